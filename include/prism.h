@@ -1,0 +1,211 @@
+/*
+ * prism.h - C ABI of the MI355X-native Prism bottleneck transformer.
+ *
+ * Drop-in for the reference's hot path: the per-block sequence
+ *   split2_qkv_attn_d256 -> moe_router -> moe_expert_skip
+ * (reference vulkan_engine/prism_moe_bench.cpp:262-291, :414-438).
+ *
+ * Conventions kept from the reference's operator surface:
+ *  - Activations are fp16, HWC, token-major: element (t, c) of a frame sits at
+ *    t*dim + c with t = y*W + x (prism_moe_bench.cpp:137, stage shaders'
+ *    coopVecLoadNV(..., (input_offset + t*dim)*2)). A batch is consecutive
+ *    frames at a stride of n_tokens*dim elements.
+ *  - Weights are one flat fp16 blob; every tensor is addressed by its ELEMENT
+ *    offset, row-major [out][in] (prism_moe_bench.cpp:164-172,
+ *    vulkan_engine/export_weights.py:96-120).
+ *  - One launch per block stage; the launch parameter structs mirror the
+ *    stages' push-constant blocks field for field, plus the pre-LayerNorm
+ *    offsets this build adds.
+ *  - Feature and aux arenas are caller-owned device buffers addressed by
+ *    element offsets, as the reference's bindings 1 (fp16 features) and 2
+ *    (int32 aux) are.
+ *
+ * Every entry point returns 0 on success or a negative PRISM_ERR_* code; no
+ * C++ exception crosses the ABI. prism_last_error() gives the message.
+ * A context is not thread-safe; calls on one context are stream-ordered.
+ * Streams are passed as void* holding a hipStream_t (NULL = default stream).
+ */
+#ifndef PRISM_H
+#define PRISM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRISM_OK               0
+#define PRISM_ERR_INVALID     -1 /* bad argument, size, offset or shape      */
+#define PRISM_ERR_UNSUPPORTED -2 /* valid but not implemented (e.g. dim 192) */
+#define PRISM_ERR_HIP         -3 /* a HIP runtime call failed                */
+#define PRISM_ERR_STATE       -4 /* e.g. weights not loaded                  */
+#define PRISM_ERR_BLOB        -5 /* weight blob or offset table inconsistent */
+#define PRISM_ERR_NOMEM       -6 /* host or device allocation failed         */
+#define PRISM_ERR_CODE_OBJECT -7 /* kernel code object missing or invalid    */
+
+/* Routing modes for the synthetic weight generator. */
+#define PRISM_ROUTE_RANDOM      0 /* router bias ~N(0, 0.02) like every bias  */
+#define PRISM_ROUTE_UNIFORM     1 /* router bias = 0 (near-uniform load)      */
+#define PRISM_ROUTE_ZIPF        2 /* bias fitted to a Zipf(1.1) expert load   */
+#define PRISM_ROUTE_ADVERSARIAL 3 /* bias fitted to 50% on expert 0, rest uniform */
+
+typedef struct prism_ctx prism_ctx;
+
+/* Model shape. n_experts == 1 is a dense block (FFN d->d->d, no router).
+ * Supported: (dim 256, 8 heads x 32) and (dim 128, 8 heads x 16); window 8;
+ * 1 <= n_experts <= 64. */
+typedef struct prism_model_desc {
+    int32_t dim, n_blocks, n_heads, head_dim, n_experts;
+    int32_t spatial_h, spatial_w, window;
+} prism_model_desc;
+
+/* Element offsets of one block's tensors in the fp16 blob. Expert e's tensors
+ * are at exp_* + e*exp_stride (prism_moe_bench.cpp:168-170). For a dense
+ * block router_w/router_b are unused. */
+typedef struct prism_block_offsets {
+    int64_t ln1_g, ln1_b, qkv_w, qkv_b, out_w, out_b;
+    int64_t ln2_g, ln2_b, router_w, router_b;
+    int64_t exp_w1, exp_b1, exp_w2, exp_b2, exp_stride;
+} prism_block_offsets;
+
+/* Attention stage parameters: shaders/split2_qkv_attn_d256.comp.glsl:11-16
+ * {n_tokens, dim, n_heads, head_dim, spatial_w, spatial_h, window_size,
+ *  qkv_w, qkv_b, out_w, out_b, input_offset, output_offset} + LN1 offsets.
+ * n_tokens is the per-frame token count and must equal spatial_w*spatial_h. */
+typedef struct prism_attn_push {
+    int32_t n_tokens, dim, n_heads, head_dim;
+    int32_t spatial_w, spatial_h, window_size;
+    int64_t qkv_w, qkv_b, out_w, out_b;
+    int64_t input_offset, output_offset;
+    int64_t ln1_g, ln1_b;
+} prism_attn_push;
+
+/* Router stage parameters: shaders/moe_router.comp.glsl:11-17
+ * {n_tokens, dim, n_experts, router_w, router_b, input_offset,
+ *  assignment_offset, count_offset} + LN2 offsets + perm_offset.
+ * aux layout: assignment [batch*n_tokens] int32 (expert id per token),
+ * counts [n_experts + 1] (tokens per expert, then a completion ticket), and
+ * perm [n_experts][batch*n_tokens] (token indices bucketed by expert: the
+ * counting sort's output). counts must be zero on entry; the expert stage
+ * returns them to zero when it has consumed them. */
+typedef struct prism_router_push {
+    int32_t n_tokens, dim, n_experts;
+    int64_t router_w, router_b;
+    int64_t input_offset;
+    int64_t assignment_offset, count_offset;
+    int64_t ln2_g, ln2_b;
+    int64_t perm_offset;
+} prism_router_push;
+
+/* Expert stage parameters: shaders/moe_expert_skip.comp.glsl:13-18
+ * {n_tokens, dim, expert_id, w1, b1, w2, b2, input_offset, output_offset,
+ *  assignment_offset}, widened to ONE launch for all experts: expert_id is
+ * replaced by n_experts + expert_stride (expert e at w1 + e*expert_stride),
+ * and the router's count/perm regions are read instead of re-scanning the
+ * assignment. n_experts == 1 with count_offset < 0 is the dense FFN stage
+ * (every token, expert 0). */
+typedef struct prism_expert_push {
+    int32_t n_tokens, dim, n_experts;
+    int64_t w1, b1, w2, b2, expert_stride;
+    int64_t input_offset, output_offset;
+    int64_t assignment_offset, count_offset;
+    int64_t ln2_g, ln2_b;
+    int64_t perm_offset;
+} prism_expert_push;
+
+/* ---- host-only helpers (no GPU needed) -------------------------------- */
+
+/* Fill offs[0..n_blocks) with the build's blob layout (the reference's bump
+ * allocator wa(), prism_moe_bench.cpp:164-172, repeated per block with the LN
+ * tensors added) and return the blob size in elements. offs may be NULL. */
+int prism_layout(const prism_model_desc* desc, prism_block_offsets* offs,
+                 int64_t* total_elems);
+
+/* Check a model description and an offset table against a blob of
+ * blob_elems fp16 elements: shapes supported, every tensor in bounds and
+ * 8-element (16-byte) aligned. */
+int prism_validate(const prism_model_desc* desc, const prism_block_offsets* offs,
+                   int64_t blob_elems);
+
+/* Synthetic weights: every W and b ~N(0, 0.02), LN gamma = 1, beta = 0, from a
+ * counter-based generator (splitmix64 + Box-Muller) keyed on (seed, tensor).
+ * The router bias follows `routing` (PRISM_ROUTE_*). Writes blob (blob_elems
+ * fp16) and offs (n_blocks entries). */
+int prism_synth_weights(const prism_model_desc* desc, uint64_t seed, int32_t routing,
+                        uint16_t* blob, int64_t blob_elems, prism_block_offsets* offs);
+
+/* n fp16 values ~N(0, std^2) from the same generator (stream selects the
+ * tensor). Activations use stream 0. */
+int prism_synth_normal_f16(uint16_t* dst, int64_t n, uint64_t seed, uint64_t stream,
+                           float std);
+
+/* Tokens per expert of an assignment array (host helper for load reports). */
+int prism_histogram(const int32_t* assign, int64_t n, int32_t n_experts, int64_t* counts);
+
+/* The device weight layout: repack a row-major fp16 matrix w[rows][k] into
+ * 16x16x32-MFMA A-operand fragments (fragment (rt, ks) = rows 16rt..16rt+15 x
+ * columns 32ks..32ks+31, 1 KiB, lane l holding w[16rt + l%16][32ks + 8(l/16)
+ * + 0..7]). Rows rows..rows_padded-1 are zero. k % 32 == 0, rows_padded % 16
+ * == 0. prism_load_weights applies this to every GEMM weight. No reference
+ * counterpart: the reference hands row-major matrices to coopVecMatMulAddNV
+ * (e.g. shaders/moe_expert_skip.comp.glsl:36-39). */
+int prism_pack_weight(const uint16_t* w, int32_t rows, int32_t k, int32_t rows_padded,
+                      uint16_t* dst);
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Create a context on HIP device `device`, loading the kernel code object
+ * from code_object_path (NULL = prism_kernels.hsaco next to this library).
+ * On failure *out is NULL and prism_last_error(NULL) has the message. */
+int prism_create(prism_ctx** out, int32_t device, const char* code_object_path);
+void prism_destroy(prism_ctx* ctx);
+const char* prism_last_error(const prism_ctx* ctx);
+
+/* Upload a weight blob (host memory, fp16, `bytes` long) laid out per offs
+ * (desc->n_blocks entries) and repack it into the device's MFMA fragment
+ * layout. Equivalent of PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611). */
+int prism_load_weights(prism_ctx* ctx, const prism_model_desc* desc, const void* blob,
+                       size_t bytes, const prism_block_offsets* offs);
+
+/* Same, reading the blob from a file (the exporter's flat .weights format). */
+int prism_load_weights_file(prism_ctx* ctx, const prism_model_desc* desc,
+                            const char* path, const prism_block_offsets* offs);
+
+/* ---- per-stage launches (one dispatch each) --------------------------- */
+
+/* features: device fp16 arena; aux: device int32 arena. The weight offsets
+ * in the push structs must name tensors of a loaded block. */
+int prism_attn(prism_ctx* ctx, const prism_attn_push* p, void* features, int32_t batch,
+               void* stream);
+int prism_router(prism_ctx* ctx, const prism_router_push* p, const void* features,
+                 int32_t* aux, int32_t batch, void* stream);
+int prism_experts(prism_ctx* ctx, const prism_expert_push* p, void* features,
+                  int32_t* aux, int32_t batch, void* stream);
+
+/* ---- whole block chain -------------------------------------------------- */
+
+/* Run all loaded blocks on `batch` frames: in and out are device fp16
+ * [batch][H*W][dim] (in is not modified). Eager launches. */
+int prism_forward(prism_ctx* ctx, const void* in, void* out, int32_t batch, void* stream);
+
+/* Same chain replayed from a hipGraph captured on the first call for this
+ * (in, out, batch, stream); later calls with the same arguments only launch
+ * the graph. */
+int prism_forward_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch,
+                        void* stream);
+
+/* Device pointer to the expert assignment of every block of the most recent
+ * forward: [n_blocks][batch*H*W] int32. */
+int prism_forward_assignments(prism_ctx* ctx, const int32_t** assign_dev,
+                              int64_t* tokens_per_block);
+
+/* aux arena size in int32 elements that a router + expert pair needs for
+ * n_experts experts and batch*n_tokens tokens when laid out as
+ * [assignment | counts+ticket | perm]. */
+int64_t prism_aux_elems(int32_t n_experts, int64_t tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PRISM_H */

@@ -1,0 +1,410 @@
+/*
+ * oracle.c - fp32 CPU restatement (OpenMP) of the Prism bottleneck block chain.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the CPU baseline
+ * of the bench. Nothing in the product links, loads or calls it.
+ *
+ * Each function cites the reference lines it restates (paths relative to the
+ * reference repository). The numerics contract it implements:
+ *   r16(v)   = round-to-nearest-even to fp16 (faithful mode only)
+ *   LN(v)    = (v - mean) / sqrt(var_biased + 1e-5) * g + b, two-pass, fp32
+ *   xn       = r16(LN1(x)); padded window slots use xn = 0
+ *              (split2_qkv_attn_d256.comp.glsl:36-37 loads the zero vector)
+ *   q,k,v    = r16(W xn + b)                         (:39-51)
+ *   s_j      = (sum_d q_d k_jd) * scale over all 64 slots of the window,
+ *              scale = 0.1767766953 for head_dim 32 (:62), 1/sqrt(hd) otherwise
+ *              (attention_windowed.comp.glsl:101)
+ *   a        = r16(sum_j exp(s_j - max) v_j / max(sum_j exp(s_j - max), 1e-6)) (:63-67)
+ *   h        = r16(r16(W_o a + b_o) + x)                 (:71-76)
+ *   hn       = r16(LN2(h))
+ *   logit_e  = r16(W_r[e] hn + b_r[e]); expert = first max (strict >)
+ *              (moe_router.comp.glsl:33-45, widened to N logits as in
+ *               moe_ffn_16exp.comp.glsl:27-34)
+ *   u        = r16(W1 hn + b1); g = r16(0.5u(1+tanh(0.7978846(u+0.044715u^3))))
+ *   y        = r16(r16(W2 g + b2) + h)                   (moe_expert_skip.comp.glsl:36-54)
+ * GEMM accumulation is fp32; the reference's coopVecMatMulAddNV accumulates in a
+ * precision its driver chooses, so that point is fixed here, not copied.
+ */
+#include "oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define LN_EPS 1e-5f
+
+/* ---------------------------------------------------------------- fp16 */
+
+static inline float r16(float v) {
+    return _cvtsh_ss(_cvtss_sh(v, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+}
+static inline float rnd(int faithful, float v) { return faithful ? r16(v) : v; }
+
+void oracle_f16_to_f32(const uint16_t* src, float* dst, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+    for (size_t i = 0; i < n; ++i) dst[i] = _cvtsh_ss(src[i]);
+}
+
+void oracle_f32_to_f16(const float* src, uint16_t* dst, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+    for (size_t i = 0; i < n; ++i)
+        dst[i] = _cvtss_sh(src[i], _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+}
+
+int oracle_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void oracle_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+/* ---------------------------------------------------------------- helpers */
+
+static void ln_row(const float* x, const float* g, const float* b, int d,
+                   int faithful, float* y) {
+    float s = 0.f;
+    for (int i = 0; i < d; ++i) s += x[i];
+    const float mean = s / (float)d;
+    float v = 0.f;
+    for (int i = 0; i < d; ++i) {
+        const float t = x[i] - mean;
+        v += t * t;
+    }
+    const float inv = 1.0f / sqrtf(v / (float)d + LN_EPS);
+    for (int i = 0; i < d; ++i) y[i] = rnd(faithful, (x[i] - mean) * inv * g[i] + b[i]);
+}
+
+void oracle_layernorm(const float* x, const float* g, const float* b, int n, int d,
+                      int round16, float* y) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; ++i) ln_row(x + (size_t)i * d, g, b, d, round16, y + (size_t)i * d);
+}
+
+static inline float gelu_tanh(float u) {
+    /* moe_expert_skip.comp.glsl:43-46 */
+    return 0.5f * u * (1.0f + tanhf(0.7978846f * (u + 0.044715f * u * u * u)));
+}
+
+void oracle_gelu(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = gelu_tanh(x[i]);
+}
+
+static inline float hsum256(__m256 v) {
+    __m128 lo = _mm256_castps256_ps128(v), hi = _mm256_extractf128_ps(v, 1);
+    lo = _mm_add_ps(lo, hi);
+    lo = _mm_add_ps(lo, _mm_movehl_ps(lo, lo));
+    lo = _mm_add_ss(lo, _mm_shuffle_ps(lo, lo, 1));
+    return _mm_cvtss_f32(lo);
+}
+
+/* y[i][o] = sum_k W[o][k] x[i][k] + b[o] (fp32 accumulate), then rounded per
+ * the faithful flag. W is row-major [M][K] ("row-major, stride K*2 bytes" in
+ * coopVecMatMulAddNV's terms); K is a multiple of 8. */
+static void gemm_xwT(const float* x, int n, int K, const float* W, const float* b,
+                     int M, float* y, int ldy, int faithful) {
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        const float* x0 = x + (size_t)(i + 0) * K;
+        const float* x1 = x + (size_t)(i + 1) * K;
+        const float* x2 = x + (size_t)(i + 2) * K;
+        const float* x3 = x + (size_t)(i + 3) * K;
+        for (int o = 0; o < M; ++o) {
+            const float* wr = W + (size_t)o * K;
+            __m256 a0 = _mm256_setzero_ps(), a1 = a0, a2 = a0, a3 = a0;
+            for (int k = 0; k < K; k += 8) {
+                const __m256 wv = _mm256_loadu_ps(wr + k);
+                a0 = _mm256_fmadd_ps(wv, _mm256_loadu_ps(x0 + k), a0);
+                a1 = _mm256_fmadd_ps(wv, _mm256_loadu_ps(x1 + k), a1);
+                a2 = _mm256_fmadd_ps(wv, _mm256_loadu_ps(x2 + k), a2);
+                a3 = _mm256_fmadd_ps(wv, _mm256_loadu_ps(x3 + k), a3);
+            }
+            const float bo = b[o];
+            y[(size_t)(i + 0) * ldy + o] = rnd(faithful, hsum256(a0) + bo);
+            y[(size_t)(i + 1) * ldy + o] = rnd(faithful, hsum256(a1) + bo);
+            y[(size_t)(i + 2) * ldy + o] = rnd(faithful, hsum256(a2) + bo);
+            y[(size_t)(i + 3) * ldy + o] = rnd(faithful, hsum256(a3) + bo);
+        }
+    }
+    for (; i < n; ++i) {
+        const float* x0 = x + (size_t)i * K;
+        for (int o = 0; o < M; ++o) {
+            const float* wr = W + (size_t)o * K;
+            __m256 a0 = _mm256_setzero_ps();
+            for (int k = 0; k < K; k += 8)
+                a0 = _mm256_fmadd_ps(_mm256_loadu_ps(wr + k), _mm256_loadu_ps(x0 + k), a0);
+            y[(size_t)i * ldy + o] = rnd(faithful, hsum256(a0) + b[o]);
+        }
+    }
+}
+
+static int check_cfg(const oracle_cfg* c) {
+    if (!c || c->dim <= 0 || c->dim % 8 || c->n_heads <= 0 || c->head_dim <= 0 ||
+        c->n_heads * c->head_dim != c->dim || c->head_dim > 64 || c->window != 8 ||
+        c->H <= 0 || c->W <= 0 || c->batch <= 0 || c->n_experts <= 0)
+        return -1;
+    return 0;
+}
+
+static float attn_scale(int head_dim) {
+    /* split2_qkv_attn_d256.comp.glsl:62 uses the literal for head_dim 32;
+     * attention_windowed.comp.glsl:101 computes 1/sqrt(head_dim). */
+    return head_dim == 32 ? 0.1767766953f : 1.0f / sqrtf((float)head_dim);
+}
+
+/* ------------------------------------------------------ attention core */
+
+/* One window, all heads. q/k/v/out are [64 slots][dim]; every slot takes part
+ * as a key (split2_qkv_attn_d256.comp.glsl:33: wt = min(64, n_tokens) = 64).
+ * Restates :53-69. */
+static void window_core(int dim, int n_heads, int hd, int faithful, const float* q,
+                        const float* k, const float* v, float* out) {
+    const float scale = attn_scale(hd);
+    for (int h = 0; h < n_heads; ++h) {
+        const int ch = h * hd;
+        for (int t = 0; t < 64; ++t) {
+            float sc[64];
+            float mx = -1e9f;
+            const float* qt = q + (size_t)t * dim + ch;
+            for (int j = 0; j < 64; ++j) {
+                const float* kj = k + (size_t)j * dim + ch;
+                float s = 0.f;
+                for (int d = 0; d < hd; ++d) s += qt[d] * kj[d];
+                s *= scale;
+                sc[j] = s;
+                if (s > mx) mx = s;
+            }
+            float se = 0.f, rr[64];
+            for (int d = 0; d < hd; ++d) rr[d] = 0.f;
+            for (int j = 0; j < 64; ++j) {
+                const float wj = expf(sc[j] - mx);
+                se += wj;
+                const float* vj = v + (size_t)j * dim + ch;
+                for (int d = 0; d < hd; ++d) rr[d] += wj * vj[d];
+            }
+            const float iv = 1.0f / fmaxf(se, 1e-6f);
+            for (int d = 0; d < hd; ++d) out[(size_t)t * dim + ch + d] = rnd(faithful, rr[d] * iv);
+        }
+    }
+}
+
+void oracle_window_attention(const oracle_cfg* c, const float* q, const float* k,
+                             const float* v, float* out) {
+    window_core(c->dim, c->n_heads, c->head_dim, c->faithful, q, k, v, out);
+}
+
+/* ------------------------------------------------------ attention stage */
+
+/* Restates split2_qkv_attn_d256.comp.glsl:24-79 with the pre-LayerNorm added:
+ * window/slot mapping :25-33, padded slots :31-37, QKV :39-51, core :53-69,
+ * out-proj + fp16 residual :71-78. */
+int oracle_attn_stage(const oracle_cfg* c, const float* w, const oracle_block_offsets* o,
+                      const float* x, float* y) {
+    if (check_cfg(c) || !w || !o || !x || !y) return -1;
+    const int d = c->dim, H = c->H, W = c->W, ws = c->window;
+    const int wx = (W + ws - 1) / ws, wy = (H + ws - 1) / ws;
+    const int n_win = wx * wy;
+    const size_t T = (size_t)H * W;
+    const int F = c->faithful;
+    const float* qkv_w = w + o->qkv_w;
+    const float* qkv_b = w + o->qkv_b;
+    const float* out_w = w + o->out_w;
+    const float* out_b = w + o->out_b;
+    const float* g1 = w + o->ln1_g;
+    const float* b1 = w + o->ln1_b;
+
+#pragma omp parallel
+    {
+        float* xn = (float*)malloc(sizeof(float) * 64 * d);
+        float* qkv = (float*)malloc(sizeof(float) * 64 * 3 * d);
+        float* q = (float*)malloc(sizeof(float) * 64 * d);
+        float* k = (float*)malloc(sizeof(float) * 64 * d);
+        float* v = (float*)malloc(sizeof(float) * 64 * d);
+        float* a = (float*)malloc(sizeof(float) * 64 * d);
+        float* po = (float*)malloc(sizeof(float) * 64 * d);
+        int gt[64], valid[64];
+#pragma omp for schedule(static)
+        for (long wi_all = 0; wi_all < (long)n_win * c->batch; ++wi_all) {
+            const int f = (int)(wi_all / n_win), wi = (int)(wi_all % n_win);
+            const float* xf = x + (size_t)f * T * d;
+            float* yf = y + (size_t)f * T * d;
+            const int wyy = wi / wx, wxx = wi % wx;
+            for (int li = 0; li < 64; ++li) {
+                const int ty = li / ws, tx = li % ws;
+                const int gy = wyy * ws + ty, gx = wxx * ws + tx;
+                valid[li] = gy < H && gx < W;
+                gt[li] = valid[li] ? gy * W + gx : 0;
+                if (valid[li])
+                    ln_row(xf + (size_t)gt[li] * d, g1, b1, d, F, xn + (size_t)li * d);
+                else
+                    memset(xn + (size_t)li * d, 0, sizeof(float) * d);
+            }
+            /* QKV rows: [0,d) = Q, [d,2d) = K, [2d,3d) = V. */
+            gemm_xwT(xn, 64, d, qkv_w, qkv_b, 3 * d, qkv, 3 * d, F);
+            for (int li = 0; li < 64; ++li) {
+                memcpy(q + (size_t)li * d, qkv + (size_t)li * 3 * d, sizeof(float) * d);
+                memcpy(k + (size_t)li * d, qkv + (size_t)li * 3 * d + d, sizeof(float) * d);
+                memcpy(v + (size_t)li * d, qkv + (size_t)li * 3 * d + 2 * d, sizeof(float) * d);
+            }
+            window_core(d, c->n_heads, c->head_dim, F, q, k, v, a);
+            gemm_xwT(a, 64, d, out_w, out_b, d, po, d, F);
+            for (int li = 0; li < 64; ++li) {
+                if (!valid[li]) continue;
+                const float* xi = xf + (size_t)gt[li] * d;
+                float* yi = yf + (size_t)gt[li] * d;
+                for (int cc = 0; cc < d; ++cc) yi[cc] = rnd(F, po[(size_t)li * d + cc] + xi[cc]);
+            }
+        }
+        free(xn); free(qkv); free(q); free(k); free(v); free(a); free(po);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------ router stage */
+
+/* Restates moe_router.comp.glsl:24-45 with N logits (the shader's coopvec<4>
+ * limits it to 4; moe_ffn_16exp.comp.glsl:27-34 shows the N-wide form) and the
+ * pre-LayerNorm added. */
+int oracle_router_stage(const oracle_cfg* c, const float* w, const oracle_block_offsets* o,
+                        const float* h, int32_t* assign, float* logits) {
+    if (check_cfg(c) || !w || !o || !h || !assign) return -1;
+    const int d = c->dim, N = c->n_experts, F = c->faithful;
+    const long n = (long)c->batch * c->H * c->W;
+    const float* g2 = w + o->ln2_g;
+    const float* b2 = w + o->ln2_b;
+    const float* rw = w + o->router_w;
+    const float* rb = w + o->router_b;
+#pragma omp parallel
+    {
+        float* hn = (float*)malloc(sizeof(float) * 16 * d);
+        float* lg = (float*)malloc(sizeof(float) * 16 * N);
+#pragma omp for schedule(static)
+        for (long t0 = 0; t0 < n; t0 += 16) {
+            const int cnt = (int)((n - t0) < 16 ? (n - t0) : 16);
+            for (int i = 0; i < cnt; ++i)
+                ln_row(h + (size_t)(t0 + i) * d, g2, b2, d, F, hn + (size_t)i * d);
+            gemm_xwT(hn, cnt, d, rw, rb, N, lg, N, F);
+            for (int i = 0; i < cnt; ++i) {
+                const float* li = lg + (size_t)i * N;
+                int best = 0;
+                float bv = li[0];
+                for (int e = 1; e < N; ++e)
+                    if (li[e] > bv) { bv = li[e]; best = e; }
+                assign[t0 + i] = best;
+                if (logits) memcpy(logits + (size_t)(t0 + i) * N, li, sizeof(float) * N);
+            }
+        }
+        free(hn); free(lg);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------ expert stage */
+
+/* Restates moe_expert_skip.comp.glsl:25-54 for all experts at once: each token
+ * runs exactly the expert it was assigned, with the pre-LayerNorm added.
+ * Tokens are grouped by expert so each expert's weights stay in cache. */
+int oracle_expert_stage(const oracle_cfg* c, const float* w, const oracle_block_offsets* o,
+                        const float* h, const int32_t* assign, float* y) {
+    if (check_cfg(c) || !w || !o || !h || !y) return -1;
+    const int d = c->dim, N = c->n_experts, F = c->faithful;
+    const long n = (long)c->batch * c->H * c->W;
+    const float* g2 = w + o->ln2_g;
+    const float* bb2 = w + o->ln2_b;
+
+    long* cnt = (long*)calloc((size_t)N + 1, sizeof(long));
+    long* order = (long*)malloc(sizeof(long) * (size_t)(n > 0 ? n : 1));
+    for (long t = 0; t < n; ++t) {
+        const int e = assign ? assign[t] : 0;
+        if (e < 0 || e >= N) { free(cnt); free(order); return -1; }
+        cnt[e + 1]++;
+    }
+    for (int e = 0; e < N; ++e) cnt[e + 1] += cnt[e];
+    long* fill = (long*)malloc(sizeof(long) * (size_t)N);
+    for (int e = 0; e < N; ++e) fill[e] = cnt[e];
+    for (long t = 0; t < n; ++t) order[fill[assign ? assign[t] : 0]++] = t;
+    free(fill);
+
+    /* Work items: chunks of up to 16 same-expert tokens. */
+    long n_items = 0;
+    for (int e = 0; e < N; ++e) n_items += (cnt[e + 1] - cnt[e] + 15) / 16;
+    long* item_start = (long*)malloc(sizeof(long) * (size_t)(n_items + 1));
+    int* item_exp = (int*)malloc(sizeof(int) * (size_t)(n_items + 1));
+    long it = 0;
+    for (int e = 0; e < N; ++e)
+        for (long s = cnt[e]; s < cnt[e + 1]; s += 16) { item_start[it] = s; item_exp[it] = e; ++it; }
+
+#pragma omp parallel
+    {
+        float* hn = (float*)malloc(sizeof(float) * 16 * d);
+        float* u = (float*)malloc(sizeof(float) * 16 * d);
+        float* yy = (float*)malloc(sizeof(float) * 16 * d);
+#pragma omp for schedule(dynamic, 4)
+        for (long i = 0; i < n_items; ++i) {
+            const int e = item_exp[i];
+            const long s0 = item_start[i];
+            const long s1 = (s0 + 16 < cnt[e + 1]) ? s0 + 16 : cnt[e + 1];
+            const int m = (int)(s1 - s0);
+            for (int r = 0; r < m; ++r)
+                ln_row(h + (size_t)order[s0 + r] * d, g2, bb2, d, F, hn + (size_t)r * d);
+            const int64_t eo = (int64_t)e * o->exp_stride;
+            gemm_xwT(hn, m, d, w + o->exp_w1 + eo, w + o->exp_b1 + eo, d, u, d, F);
+            for (int r = 0; r < m * d; ++r) u[r] = rnd(F, gelu_tanh(u[r]));
+            gemm_xwT(u, m, d, w + o->exp_w2 + eo, w + o->exp_b2 + eo, d, yy, d, F);
+            for (int r = 0; r < m; ++r) {
+                const float* hr = h + (size_t)order[s0 + r] * d;
+                float* yr = y + (size_t)order[s0 + r] * d;
+                for (int cc = 0; cc < d; ++cc) yr[cc] = rnd(F, yy[(size_t)r * d + cc] + hr[cc]);
+            }
+        }
+        free(hn); free(u); free(yy);
+    }
+    free(cnt); free(order); free(item_start); free(item_exp);
+    return 0;
+}
+
+/* ------------------------------------------------------ block chain */
+
+/* prism_moe_bench.cpp:414-438: per block attn -> router -> experts, then the
+ * output feeds the next block. The input is left untouched here. */
+int oracle_forward(const oracle_cfg* c, const float* w, const oracle_block_offsets* offs,
+                   int n_blocks, const float* x, float* y, int32_t* assign_out, float* h_out) {
+    if (check_cfg(c) || !w || !offs || !x || !y || n_blocks <= 0) return -1;
+    const size_t n = (size_t)c->batch * c->H * c->W;
+    const size_t elems = n * (size_t)c->dim;
+    float* hb = (float*)malloc(sizeof(float) * elems);
+    float* cur = (float*)malloc(sizeof(float) * elems);
+    int32_t* as = (int32_t*)malloc(sizeof(int32_t) * n);
+    if (!hb || !cur || !as) { free(hb); free(cur); free(as); return -2; }
+    memcpy(cur, x, sizeof(float) * elems);
+    int rc = 0;
+    for (int b = 0; b < n_blocks && !rc; ++b) {
+        rc = oracle_attn_stage(c, w, &offs[b], cur, hb);
+        if (rc) break;
+        if (h_out) memcpy(h_out + (size_t)b * elems, hb, sizeof(float) * elems);
+        if (c->n_experts > 1) {
+            rc = oracle_router_stage(c, w, &offs[b], hb, as, NULL);
+            if (rc) break;
+            if (assign_out) memcpy(assign_out + (size_t)b * n, as, sizeof(int32_t) * n);
+        } else {
+            memset(as, 0, sizeof(int32_t) * n);
+            if (assign_out) memset(assign_out + (size_t)b * n, 0, sizeof(int32_t) * n);
+        }
+        rc = oracle_expert_stage(c, w, &offs[b], hb, as, cur);
+    }
+    if (!rc) memcpy(y, cur, sizeof(float) * elems);
+    free(hb); free(cur); free(as);
+    return rc;
+}

@@ -1,0 +1,635 @@
+/*
+ * engine.cpp - host engine: code object, weights, per-stage launches, block
+ * chain and its hipGraph.
+ *
+ * Mirrors the reference's engine surface (vulkan_engine/prism_vulkan.h:73-117:
+ * Init / LoadWeights / RecordCommandBuffer / InferGPU) and the MoE bench's
+ * per-block recording (prism_moe_bench.cpp:262-291): kernels come from one
+ * code object (hipModuleLoad, the analogue of loadPipeline(".spv")), each
+ * stage is one hipModuleLaunchKernel, and the per-frame block chain is
+ * captured once into a hipGraph (the analogue of the once-recorded command
+ * buffer that is re-submitted every frame, prism_moe_bench.cpp:183-209).
+ */
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <string>
+#include <vector>
+
+#include "../kernel_args.h"
+#include "engine_internal.h"
+
+namespace prism {
+
+static thread_local std::string g_error;
+void set_global_error(const std::string& msg) { g_error = msg; }
+
+struct DevBlock {
+    prism_block_offsets offs;
+    uint16_t* wqkv;
+    float* bqkv;
+    uint16_t* wo;
+    float* bo;
+    float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+    uint16_t* wr;
+    float* br;
+    uint16_t* w1;
+    float* b1;
+    uint16_t* w2;
+    float* b2;
+};
+
+}  // namespace prism
+
+using namespace prism;
+
+struct prism_ctx {
+    int device = 0;
+    hipModule_t module = nullptr;
+    hipFunction_t f_attn[2] = {};       /* [0] d128, [1] d256 */
+    hipFunction_t f_router[2] = {};
+    hipFunction_t f_expert[2][2] = {};  /* [dim][bm64, bm128] */
+    std::string err;
+
+    bool loaded = false;
+    prism_model_desc desc{};
+    void* warena = nullptr;
+    std::vector<DevBlock> blocks;
+
+    /* forward workspace */
+    void* ws = nullptr;
+    int ws_batch = 0;
+    uint16_t* ws_attn = nullptr;
+    uint16_t* ws_scratch = nullptr;
+    int32_t* ws_assign = nullptr; /* [n_blocks][n] */
+    int32_t* ws_counts = nullptr; /* [N + 1] */
+    int32_t* ws_perm = nullptr;   /* [N][n] */
+    int64_t ws_tokens = 0;
+    int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
+
+    hipStream_t cap_stream = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    const void* g_in = nullptr;
+    void* g_out = nullptr;
+    int g_batch = 0;
+};
+
+static int fail(prism_ctx* c, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    g_error = buf;
+    return code;
+}
+
+#define HIP_TRY(ctx, call)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail((ctx), PRISM_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static int dim_index(int dim) { return dim == 256 ? 1 : 0; }
+
+static std::string default_code_object() {
+    Dl_info info;
+    if (dladdr((void*)&prism_create, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        const size_t s = p.find_last_of('/');
+        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) + "/prism_kernels.hsaco";
+    }
+    return "prism_kernels.hsaco";
+}
+
+/* ------------------------------------------------------------ lifecycle */
+
+extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_object_path) {
+    if (!out) return fail(nullptr, PRISM_ERR_INVALID, "prism_create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return fail(nullptr, PRISM_ERR_HIP, "no HIP device available (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n)
+        return fail(nullptr, PRISM_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+    const std::string path = code_object_path ? std::string(code_object_path) : default_code_object();
+    {
+        std::ifstream f(path, std::ios::binary);
+        if (!f.good()) return fail(nullptr, PRISM_ERR_CODE_OBJECT, "code object not found: %s", path.c_str());
+    }
+    prism_ctx* c = new prism_ctx();
+    c->device = device;
+    e = hipSetDevice(device);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, PRISM_ERR_HIP, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+    }
+    e = hipModuleLoad(&c->module, path.c_str());
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, PRISM_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    struct { hipFunction_t* f; const char* name; } fns[] = {
+        {&c->f_attn[0], "prism_attn_d128"},           {&c->f_attn[1], "prism_attn_d256"},
+        {&c->f_router[0], "prism_router_d128"},       {&c->f_router[1], "prism_router_d256"},
+        {&c->f_expert[0][0], "prism_expert_d128_bm64"}, {&c->f_expert[0][1], "prism_expert_d128_bm128"},
+        {&c->f_expert[1][0], "prism_expert_d256_bm64"}, {&c->f_expert[1][1], "prism_expert_d256_bm128"},
+    };
+    for (auto& f : fns) {
+        e = hipModuleGetFunction(f.f, c->module, f.name);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(c->module);
+            delete c;
+            return fail(nullptr, PRISM_ERR_CODE_OBJECT, "kernel %s missing from %s: %s", f.name, path.c_str(),
+                        hipGetErrorString(e));
+        }
+    }
+    e = hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        (void)hipModuleUnload(c->module);
+        delete c;
+        return fail(nullptr, PRISM_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    *out = c;
+    return PRISM_OK;
+}
+
+static void drop_graph(prism_ctx* c) {
+    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->gexec = nullptr;
+    c->graph = nullptr;
+    c->g_in = nullptr;
+    c->g_out = nullptr;
+    c->g_batch = 0;
+}
+
+static void drop_workspace(prism_ctx* c) {
+    if (c->ws) (void)hipFree(c->ws);
+    c->ws = nullptr;
+    c->ws_batch = 0;
+    c->ws_tokens = 0;
+}
+
+extern "C" void prism_destroy(prism_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipDeviceSynchronize();
+    drop_graph(c);
+    drop_workspace(c);
+    if (c->warena) (void)hipFree(c->warena);
+    if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
+    if (c->module) (void)hipModuleUnload(c->module);
+    delete c;
+}
+
+extern "C" const char* prism_last_error(const prism_ctx* c) { return c ? c->err.c_str() : g_error.c_str(); }
+
+/* ------------------------------------------------------------ weights */
+
+namespace {
+
+struct Arena {
+    size_t off = 0;
+    size_t take(size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) & ~size_t(255);
+        return o;
+    }
+};
+
+struct BlockPlan {
+    size_t wqkv, bqkv, wo, bo, ln1_g, ln1_b, ln2_g, ln2_b, wr, br, w1, b1, w2, b2;
+};
+
+inline int round16(int n) { return (n + 15) & ~15; }
+
+}  // namespace
+
+extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const void* blob, size_t bytes,
+                                  const prism_block_offsets* offs) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!blob) return fail(c, PRISM_ERR_INVALID, "weight blob is NULL");
+    if (bytes % 2) return fail(c, PRISM_ERR_BLOB, "blob size %zu is not a whole number of fp16 values", bytes);
+    std::string why;
+    const int rc = validate_blocks(d, offs, (int64_t)(bytes / 2), &why);
+    if (rc) return fail(c, rc, "%s", why.c_str());
+    HIP_TRY(c, hipSetDevice(c->device));
+
+    const int D = d->dim, N = d->n_experts, NP = N > 1 ? round16(N) : 0;
+    const uint16_t* src = static_cast<const uint16_t*>(blob);
+    Arena ar;
+    std::vector<BlockPlan> plan(d->n_blocks);
+    for (int b = 0; b < d->n_blocks; ++b) {
+        BlockPlan& p = plan[b];
+        p.wqkv = ar.take(3ull * D * D * 2);
+        p.bqkv = ar.take(3ull * D * 4);
+        p.wo = ar.take(1ull * D * D * 2);
+        p.bo = ar.take(D * 4);
+        p.ln1_g = ar.take(D * 4);
+        p.ln1_b = ar.take(D * 4);
+        p.ln2_g = ar.take(D * 4);
+        p.ln2_b = ar.take(D * 4);
+        p.wr = ar.take((size_t)NP * D * 2);
+        p.br = ar.take((size_t)NP * 4);
+        p.w1 = ar.take((size_t)N * D * D * 2);
+        p.b1 = ar.take((size_t)N * D * 4);
+        p.w2 = ar.take((size_t)N * D * D * 2);
+        p.b2 = ar.take((size_t)N * D * 4);
+    }
+    std::vector<uint8_t> host;
+    try {
+        host.assign(ar.off, 0);
+    } catch (...) {
+        return fail(c, PRISM_ERR_NOMEM, "cannot allocate %zu bytes of host staging", ar.off);
+    }
+    auto f32 = [&](size_t at, const uint16_t* s, int n) {
+        float* dst = reinterpret_cast<float*>(host.data() + at);
+        for (int i = 0; i < n; ++i) dst[i] = half_to_float(s[i]);
+    };
+    for (int b = 0; b < d->n_blocks; ++b) {
+        const BlockPlan& p = plan[b];
+        const prism_block_offsets& o = offs[b];
+        pack_fragments(src + o.qkv_w, 3 * D, D, 3 * D, reinterpret_cast<uint16_t*>(host.data() + p.wqkv));
+        f32(p.bqkv, src + o.qkv_b, 3 * D);
+        pack_fragments(src + o.out_w, D, D, D, reinterpret_cast<uint16_t*>(host.data() + p.wo));
+        f32(p.bo, src + o.out_b, D);
+        f32(p.ln1_g, src + o.ln1_g, D);
+        f32(p.ln1_b, src + o.ln1_b, D);
+        f32(p.ln2_g, src + o.ln2_g, D);
+        f32(p.ln2_b, src + o.ln2_b, D);
+        if (N > 1) {
+            pack_fragments(src + o.router_w, N, D, NP, reinterpret_cast<uint16_t*>(host.data() + p.wr));
+            float* br = reinterpret_cast<float*>(host.data() + p.br);
+            for (int e = 0; e < NP; ++e) br[e] = e < N ? half_to_float(src[o.router_b + e]) : -INFINITY;
+        }
+        for (int e = 0; e < N; ++e) {
+            const int64_t eo = (int64_t)e * o.exp_stride;
+            pack_fragments(src + o.exp_w1 + eo, D, D, D,
+                           reinterpret_cast<uint16_t*>(host.data() + p.w1) + (size_t)e * D * D);
+            pack_fragments(src + o.exp_w2 + eo, D, D, D,
+                           reinterpret_cast<uint16_t*>(host.data() + p.w2) + (size_t)e * D * D);
+            f32(p.b1 + (size_t)e * D * 4, src + o.exp_b1 + eo, D);
+            f32(p.b2 + (size_t)e * D * 4, src + o.exp_b2 + eo, D);
+        }
+    }
+
+    (void)hipDeviceSynchronize();
+    drop_graph(c);
+    if (c->warena) {
+        (void)hipFree(c->warena);
+        c->warena = nullptr;
+    }
+    c->loaded = false;
+    void* arena = nullptr;
+    hipError_t e = hipMalloc(&arena, ar.off);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for weights: %s", ar.off, hipGetErrorString(e));
+    e = hipMemcpy(arena, host.data(), ar.off, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(arena);
+        return fail(c, PRISM_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+    }
+    c->warena = arena;
+    c->blocks.assign(d->n_blocks, DevBlock{});
+    uint8_t* base = static_cast<uint8_t*>(arena);
+    for (int b = 0; b < d->n_blocks; ++b) {
+        const BlockPlan& p = plan[b];
+        DevBlock& k = c->blocks[b];
+        k.offs = offs[b];
+        k.wqkv = reinterpret_cast<uint16_t*>(base + p.wqkv);
+        k.bqkv = reinterpret_cast<float*>(base + p.bqkv);
+        k.wo = reinterpret_cast<uint16_t*>(base + p.wo);
+        k.bo = reinterpret_cast<float*>(base + p.bo);
+        k.ln1_g = reinterpret_cast<float*>(base + p.ln1_g);
+        k.ln1_b = reinterpret_cast<float*>(base + p.ln1_b);
+        k.ln2_g = reinterpret_cast<float*>(base + p.ln2_g);
+        k.ln2_b = reinterpret_cast<float*>(base + p.ln2_b);
+        k.wr = N > 1 ? reinterpret_cast<uint16_t*>(base + p.wr) : nullptr;
+        k.br = N > 1 ? reinterpret_cast<float*>(base + p.br) : nullptr;
+        k.w1 = reinterpret_cast<uint16_t*>(base + p.w1);
+        k.b1 = reinterpret_cast<float*>(base + p.b1);
+        k.w2 = reinterpret_cast<uint16_t*>(base + p.w2);
+        k.b2 = reinterpret_cast<float*>(base + p.b2);
+    }
+    if (c->desc.n_experts != d->n_experts || c->desc.dim != d->dim || c->desc.n_blocks != d->n_blocks ||
+        c->desc.spatial_h != d->spatial_h || c->desc.spatial_w != d->spatial_w)
+        drop_workspace(c);
+    c->desc = *d;
+    c->loaded = true;
+    return PRISM_OK;
+}
+
+extern "C" int prism_load_weights_file(prism_ctx* c, const prism_model_desc* d, const char* path,
+                                       const prism_block_offsets* offs) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!path) return fail(c, PRISM_ERR_INVALID, "path is NULL");
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    if (!f.is_open()) return fail(c, PRISM_ERR_INVALID, "cannot open %s", path);
+    const std::streamsize size = f.tellg();
+    f.seekg(0);
+    std::vector<char> data;
+    try {
+        data.resize((size_t)size);
+    } catch (...) {
+        return fail(c, PRISM_ERR_NOMEM, "cannot allocate %lld bytes for %s", (long long)size, path);
+    }
+    if (size > 0 && !f.read(data.data(), size)) return fail(c, PRISM_ERR_INVALID, "short read on %s", path);
+    return prism_load_weights(c, d, data.data(), data.size(), offs);
+}
+
+/* ------------------------------------------------------------ launches */
+
+namespace {
+
+template <class A>
+int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s) {
+    void* params[] = {&args};
+    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+    return PRISM_OK;
+}
+
+int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
+                 hipStream_t s) {
+    const int D = c->desc.dim;
+    AttnArgs a{};
+    a.in = in;
+    a.out = out;
+    a.wqkv = k.wqkv;
+    a.bqkv = k.bqkv;
+    a.wo = k.wo;
+    a.bo = k.bo;
+    a.ln_g = k.ln1_g;
+    a.ln_b = k.ln1_b;
+    a.frame_elems = (int64_t)H * W * D;
+    a.H = H;
+    a.W = W;
+    a.wx = (W + 7) / 8;
+    a.windows_per_frame = a.wx * ((H + 7) / 8);
+    const int64_t grid = (int64_t)a.windows_per_frame * batch;
+    if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "attention grid %lld out of range", (long long)grid);
+    return launch(c, c->f_attn[dim_index(D)], (unsigned)grid, a, s);
+}
+
+int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t* assign, int32_t* counts,
+                   int32_t* perm, int64_t n, hipStream_t s) {
+    const int N = c->desc.n_experts;
+    RouterArgs a{};
+    a.in = in;
+    a.ln_g = k.ln2_g;
+    a.ln_b = k.ln2_b;
+    a.wr = k.wr;
+    a.br = k.br;
+    a.assign = assign;
+    a.counts = counts;
+    a.perm = perm;
+    a.n_tokens = (int32_t)n;
+    a.n_experts = N;
+    a.np = round16(N);
+    a.cap = (int32_t)n;
+    const int64_t grid = (n + 127) / 128;
+    return launch(c, c->f_router[dim_index(c->desc.dim)], (unsigned)grid, a, s);
+}
+
+int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int32_t* counts,
+                    const int32_t* perm, int64_t n, hipStream_t s) {
+    const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
+    ExpertArgs a{};
+    a.in = in;
+    a.out = out;
+    a.ln_g = k.ln2_g;
+    a.ln_b = k.ln2_b;
+    a.w1 = k.w1;
+    a.b1 = k.b1;
+    a.w2 = k.w2;
+    a.b2 = k.b2;
+    a.counts = counts;
+    a.perm = perm;
+    a.n_tokens = (int32_t)n;
+    a.n_experts = N;
+    a.cap = (int32_t)n;
+    const int bm_idx = n >= 65536 ? 1 : 0;
+    const int64_t bm = bm_idx ? 128 : 64;
+    int64_t tiles = (n + bm - 1) / bm + (counts ? N : 0);
+    tiles = (tiles + 7) / 8 * 8;
+    return launch(c, c->f_expert[dim_index(D)][bm_idx], (unsigned)tiles, a, s);
+}
+
+/* which: 0 = attention (qkv_w), 1 = router (router_w), 2 = experts (exp_w1) */
+const DevBlock* find_block(prism_ctx* c, int64_t key, int which) {
+    for (const DevBlock& k : c->blocks) {
+        const int64_t v = which == 0 ? k.offs.qkv_w : which == 1 ? k.offs.router_w : k.offs.exp_w1;
+        if (v == key) return &k;
+    }
+    return nullptr;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int prism_attn(prism_ctx* c, const prism_attn_push* p, void* features, int32_t batch, void* stream) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
+    if (!p || !features) return fail(c, PRISM_ERR_INVALID, "push or features is NULL");
+    if (batch < 1) return fail(c, PRISM_ERR_INVALID, "batch %d < 1", batch);
+    if (p->dim != c->desc.dim || p->n_heads != c->desc.n_heads || p->head_dim != c->desc.head_dim)
+        return fail(c, PRISM_ERR_INVALID, "push shape dim=%d heads=%d head_dim=%d does not match the loaded model", p->dim,
+                    p->n_heads, p->head_dim);
+    if (p->window_size != 8) return fail(c, PRISM_ERR_UNSUPPORTED, "window_size %d (supported: 8)", p->window_size);
+    if (p->spatial_w < 1 || p->spatial_h < 1 || (int64_t)p->spatial_w * p->spatial_h != p->n_tokens)
+        return fail(c, PRISM_ERR_INVALID, "n_tokens %d != spatial_w*spatial_h (%d*%d)", p->n_tokens, p->spatial_w,
+                    p->spatial_h);
+    const DevBlock* k = find_block(c, p->qkv_w, 0);
+    if (!k || k->offs.qkv_b != p->qkv_b || k->offs.out_w != p->out_w || k->offs.out_b != p->out_b ||
+        k->offs.ln1_g != p->ln1_g || k->offs.ln1_b != p->ln1_b)
+        return fail(c, PRISM_ERR_INVALID, "attention weight offsets do not name a loaded block");
+    if (p->input_offset < 0 || p->output_offset < 0)
+        return fail(c, PRISM_ERR_INVALID, "negative feature offset");
+    uint16_t* f = static_cast<uint16_t*>(features);
+    if (!aligned16(f + p->input_offset) || !aligned16(f + p->output_offset))
+        return fail(c, PRISM_ERR_INVALID, "feature offsets must be 16-byte aligned (multiples of 8 elements)");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return enqueue_attn(c, *k, f + p->input_offset, f + p->output_offset, p->spatial_h, p->spatial_w, batch,
+                        (hipStream_t)stream);
+}
+
+extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void* features, int32_t* aux,
+                            int32_t batch, void* stream) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
+    if (!p || !features || !aux) return fail(c, PRISM_ERR_INVALID, "push, features or aux is NULL");
+    if (c->desc.n_experts < 2) return fail(c, PRISM_ERR_STATE, "the loaded model is dense (no router)");
+    if (batch < 1 || p->n_tokens < 1) return fail(c, PRISM_ERR_INVALID, "batch %d / n_tokens %d < 1", batch, p->n_tokens);
+    if (p->dim != c->desc.dim || p->n_experts != c->desc.n_experts)
+        return fail(c, PRISM_ERR_INVALID, "push dim=%d n_experts=%d does not match the loaded model", p->dim, p->n_experts);
+    const int64_t n = (int64_t)batch * p->n_tokens;
+    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    const DevBlock* k = find_block(c, p->router_w, 1);
+    if (!k || k->offs.router_b != p->router_b || k->offs.ln2_g != p->ln2_g || k->offs.ln2_b != p->ln2_b)
+        return fail(c, PRISM_ERR_INVALID, "router weight offsets do not name a loaded block");
+    if (p->input_offset < 0 || p->assignment_offset < 0 || p->count_offset < 0 || p->perm_offset < 0)
+        return fail(c, PRISM_ERR_INVALID, "negative offset");
+    const uint16_t* f = static_cast<const uint16_t*>(features);
+    if (!aligned16(f + p->input_offset)) return fail(c, PRISM_ERR_INVALID, "input_offset must be a multiple of 8");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return enqueue_router(c, *k, f + p->input_offset, aux + p->assignment_offset, aux + p->count_offset,
+                          aux + p->perm_offset, n, (hipStream_t)stream);
+}
+
+extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* features, int32_t* aux, int32_t batch,
+                             void* stream) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
+    if (!p || !features) return fail(c, PRISM_ERR_INVALID, "push or features is NULL");
+    if (batch < 1 || p->n_tokens < 1) return fail(c, PRISM_ERR_INVALID, "batch %d / n_tokens %d < 1", batch, p->n_tokens);
+    const bool dense = p->count_offset < 0;
+    if (p->dim != c->desc.dim) return fail(c, PRISM_ERR_INVALID, "push dim %d does not match the model", p->dim);
+    if (dense ? p->n_experts != 1 : p->n_experts != c->desc.n_experts)
+        return fail(c, PRISM_ERR_INVALID, "n_experts %d does not match the model (%d) / dense mode", p->n_experts,
+                    c->desc.n_experts);
+    if (!dense && (!aux || p->perm_offset < 0))
+        return fail(c, PRISM_ERR_INVALID, "routed expert stage needs aux with count and perm regions");
+    const int64_t n = (int64_t)batch * p->n_tokens;
+    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    const DevBlock* k = find_block(c, p->w1, 2);
+    if (!k || k->offs.exp_b1 != p->b1 || k->offs.exp_w2 != p->w2 || k->offs.exp_b2 != p->b2 ||
+        k->offs.exp_stride != p->expert_stride || k->offs.ln2_g != p->ln2_g || k->offs.ln2_b != p->ln2_b)
+        return fail(c, PRISM_ERR_INVALID, "expert weight offsets do not name a loaded block");
+    if (p->input_offset < 0 || p->output_offset < 0) return fail(c, PRISM_ERR_INVALID, "negative feature offset");
+    uint16_t* f = static_cast<uint16_t*>(features);
+    if (!aligned16(f + p->input_offset) || !aligned16(f + p->output_offset))
+        return fail(c, PRISM_ERR_INVALID, "feature offsets must be multiples of 8 elements");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return enqueue_experts(c, *k, f + p->input_offset, f + p->output_offset, dense ? nullptr : aux + p->count_offset,
+                           dense ? nullptr : aux + p->perm_offset, n, (hipStream_t)stream);
+}
+
+/* ------------------------------------------------------------ block chain */
+
+static int ensure_workspace(prism_ctx* c, int batch) {
+    if (c->ws && c->ws_batch >= batch) return PRISM_OK;
+    drop_graph(c);
+    drop_workspace(c);
+    const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
+    const int D = c->desc.dim, N = c->desc.n_experts, NB = c->desc.n_blocks;
+    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    Arena ar;
+    const size_t o_attn = ar.take((size_t)n * D * 2);
+    const size_t o_scr = ar.take((size_t)n * D * 2);
+    const size_t o_asg = ar.take((size_t)NB * n * 4);
+    const size_t o_cnt = ar.take((size_t)(N + 1) * 4);
+    const size_t o_perm = ar.take((size_t)N * n * 4);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, ar.off);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for the workspace: %s", ar.off, hipGetErrorString(e));
+    e = hipMemset(p, 0, ar.off);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return fail(c, PRISM_ERR_HIP, "hipMemset workspace: %s", hipGetErrorString(e));
+    }
+    uint8_t* b = static_cast<uint8_t*>(p);
+    c->ws = p;
+    c->ws_batch = batch;
+    c->ws_tokens = n;
+    c->ws_attn = reinterpret_cast<uint16_t*>(b + o_attn);
+    c->ws_scratch = reinterpret_cast<uint16_t*>(b + o_scr);
+    c->ws_assign = reinterpret_cast<int32_t*>(b + o_asg);
+    c->ws_counts = reinterpret_cast<int32_t*>(b + o_cnt);
+    c->ws_perm = reinterpret_cast<int32_t*>(b + o_perm);
+    return PRISM_OK;
+}
+
+/* Block b reads the previous block's output (block 0 reads `in`) and writes
+ * `out` if (n_blocks-1-b) is even, the scratch buffer otherwise, so the last
+ * block always lands in `out` and `in` is only read. */
+static int enqueue_forward(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
+    const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w;
+    const int64_t n = (int64_t)batch * H * W;
+    const bool moe = c->desc.n_experts > 1;
+    c->fwd_tokens = n;
+    const uint16_t* src = in;
+    for (int b = 0; b < NB; ++b) {
+        const DevBlock& k = c->blocks[b];
+        uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : c->ws_scratch;
+        int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s);
+        if (rc) return rc;
+        if (moe) {
+            rc = enqueue_router(c, k, c->ws_attn, c->ws_assign + (size_t)b * n, c->ws_counts, c->ws_perm, n, s);
+            if (rc) return rc;
+            rc = enqueue_experts(c, k, c->ws_attn, dst, c->ws_counts, c->ws_perm, n, s);
+        } else {
+            rc = enqueue_experts(c, k, c->ws_attn, dst, nullptr, nullptr, n, s);
+        }
+        if (rc) return rc;
+        src = dst;
+    }
+    return PRISM_OK;
+}
+
+static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
+    if (!in || !out) return fail(c, PRISM_ERR_INVALID, "in or out is NULL");
+    if (!aligned16(in) || !aligned16(out)) return fail(c, PRISM_ERR_INVALID, "in/out must be 16-byte aligned");
+    if (batch < 1) return fail(c, PRISM_ERR_INVALID, "batch %d < 1", batch);
+    return PRISM_OK;
+}
+
+extern "C" int prism_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    int rc = forward_checks(c, in, out, batch);
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    rc = ensure_workspace(c, batch);
+    if (rc) return rc;
+    return enqueue_forward(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
+                           (hipStream_t)stream);
+}
+
+extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    int rc = forward_checks(c, in, out, batch);
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (!(c->gexec && c->g_in == in && c->g_out == out && c->g_batch == batch)) {
+        rc = ensure_workspace(c, batch);
+        if (rc) return rc;
+        drop_graph(c);
+        HIP_TRY(c, hipStreamSynchronize(c->cap_stream));
+        HIP_TRY(c, hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
+        rc = enqueue_forward(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, c->cap_stream);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(c->cap_stream, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+        c->graph = g;
+        const hipError_t ei = hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0);
+        if (ei != hipSuccess) {
+            drop_graph(c);
+            return fail(c, PRISM_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ei));
+        }
+        c->g_in = in;
+        c->g_out = out;
+        c->g_batch = batch;
+    }
+    HIP_TRY(c, hipGraphLaunch(c->gexec, (hipStream_t)stream));
+    return PRISM_OK;
+}
+
+extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_dev, int64_t* tokens_per_block) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->ws) return fail(c, PRISM_ERR_STATE, "no forward has run");
+    if (assign_dev) *assign_dev = c->ws_assign;
+    if (tokens_per_block) *tokens_per_block = c->fwd_tokens;
+    return PRISM_OK;
+}

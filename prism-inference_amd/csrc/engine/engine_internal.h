@@ -1,0 +1,25 @@
+/* engine_internal.h - declarations shared by the host engine's translation units. */
+#ifndef PRISM_ENGINE_INTERNAL_H
+#define PRISM_ENGINE_INTERNAL_H
+
+#include <cstdint>
+#include <string>
+
+#include "prism.h"
+
+namespace prism {
+
+bool shape_supported(const prism_model_desc* d, std::string* why);
+int64_t layout_blocks(const prism_model_desc* d, prism_block_offsets* offs);
+int validate_blocks(const prism_model_desc* d, const prism_block_offsets* offs, int64_t total,
+                    std::string* why);
+void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst);
+float half_to_float(uint16_t h);
+uint16_t float_to_half(float f);
+
+/* thread-local message for calls that have no context (create, host helpers) */
+void set_global_error(const std::string& msg);
+
+}  // namespace prism
+
+#endif

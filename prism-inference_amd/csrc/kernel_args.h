@@ -1,0 +1,66 @@
+/*
+ * kernel_args.h - argument blocks passed by value to the gfx950 kernels.
+ *
+ * Shared by the host engine (which fills them and launches through
+ * hipModuleLaunchKernel) and the device code. Plain C, no HIP types.
+ *
+ * Packed weight format ("A-fragment order"): a row-major fp16 matrix
+ * W[rows][K] is stored as fragments of the 16x16x32 fp16 MFMA. Fragment
+ * (rt, ks) covers rows 16*rt .. 16*rt+15 and columns 32*ks .. 32*ks+31 and is
+ * 64 lanes x 8 halfs = 1 KiB contiguous; lane l holds
+ *   W[16*rt + (l & 15)][32*ks + 8*(l >> 4) + j],  j = 0..7
+ * at halfs ((rt*KS + ks)*64 + l)*8 + j, KS = K/32. One wave reads one
+ * fragment with one fully coalesced 16-byte load per lane.
+ */
+#ifndef PRISM_KERNEL_ARGS_H
+#define PRISM_KERNEL_ARGS_H
+#include <stdint.h>
+
+typedef struct AttnArgs {
+    const uint16_t* in;   /* features + input_offset (fp16 HWC)         */
+    uint16_t* out;        /* features + output_offset                   */
+    const uint16_t* wqkv; /* packed [3*dim/16][dim/32] fragments         */
+    const float* bqkv;    /* [3*dim]                                     */
+    const uint16_t* wo;   /* packed [dim/16][dim/32]                     */
+    const float* bo;      /* [dim]                                       */
+    const float* ln_g;    /* [dim]                                       */
+    const float* ln_b;    /* [dim]                                       */
+    int64_t frame_elems;  /* H*W*dim                                     */
+    int32_t H, W;         /* token grid                                  */
+    int32_t wx;           /* windows per row = ceil(W/8)                 */
+    int32_t windows_per_frame;
+} AttnArgs;
+
+typedef struct RouterArgs {
+    const uint16_t* in;   /* features + input_offset                     */
+    const float* ln_g;
+    const float* ln_b;
+    const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts are 0 */
+    const float* br;      /* [np]; entries >= n_experts are -inf          */
+    int32_t* assign;      /* [n_tokens] expert id                         */
+    int32_t* counts;      /* [n_experts + 1]: per-expert totals, ticket   */
+    int32_t* perm;        /* [n_experts][cap] token ids bucketed by expert */
+    int32_t n_tokens;     /* tokens in this launch (batch * per-frame)     */
+    int32_t n_experts;
+    int32_t np;           /* n_experts rounded up to 16                    */
+    int32_t cap;          /* bucket capacity = n_tokens                    */
+} RouterArgs;
+
+typedef struct ExpertArgs {
+    const uint16_t* in;   /* h: features + input_offset                   */
+    uint16_t* out;        /* features + output_offset                     */
+    const float* ln_g;
+    const float* ln_b;
+    const uint16_t* w1;   /* packed, expert e at + e*dim*dim halfs        */
+    const float* b1;      /* [n_experts][dim]                             */
+    const uint16_t* w2;
+    const float* b2;
+    int32_t* counts;      /* NULL = dense stage (every token, expert 0)   */
+    const int32_t* perm;  /* [n_experts][cap]                             */
+    int32_t n_tokens;
+    int32_t n_experts;
+    int32_t cap;
+    int32_t pad_;
+} ExpertArgs;
+
+#endif

@@ -1,0 +1,204 @@
+/*
+ * expert.hpp - expert stage as ONE grouped GEMM launch over all experts.
+ *
+ * Restates shaders/moe_expert_skip.comp.glsl:25-54 (u = r16(W1 hn + b1),
+ * g = r16(GELU-tanh(u)), y = r16(W2 g + b2), out = r16(y + input)) with the
+ * pre-LayerNorm added. The reference launches it once per expert over every
+ * token and lets unassigned threads return (prism_moe_bench.cpp:280-287);
+ * here a workgroup takes one BM-token tile of ONE expert's segment of the
+ * router's buckets, so every lane computes.
+ *
+ * Tile scheduler: the grid is sized for the worst case (ceil(T/BM) + N tiles,
+ * rounded up to a multiple of 8). Workgroup i maps to logical tile
+ * (i % 8) * (grid / 8) + i / 8 so that consecutive tiles of one expert land on
+ * the same XCD (hardware dispatches workgroups round-robin over the 8 XCDs)
+ * and share that XCD's L2 copy of the expert's weights. Wave 0 turns the
+ * per-expert counts into a tile prefix sum and finds its (expert, row block);
+ * tiles past the end do nothing.
+ *
+ * Counts ticket: every workgroup, active or not, takes a ticket at the end;
+ * the last one returns counts[0..N] to zero for the next router launch.
+ *
+ * GEMMs are C^T = W * A^T (weights as the A operand, tokens as columns), so a
+ * lane's accumulator holds 4 consecutive channels of one token: 8-byte LDS
+ * writes for the GELU tile and 8-byte global stores for the output rows,
+ * scattered straight back to the token's HWC position (fused unpermute).
+ */
+#pragma once
+#include "common.hpp"
+
+template <int DIM, int BM>
+__device__ __forceinline__ void expert_body(const ExpertArgs& a) {
+    constexpr int KS = DIM / 32;
+    constexpr int LDS = DIM + 8;
+    constexpr int TT = BM / 16;   /* token tiles per workgroup        */
+    constexpr int RT = DIM / 64;  /* 16-row output tiles per wave     */
+    constexpr int LPS = DIM / 16; /* LN lanes per row                 */
+    constexpr int RPI = 64 / LPS; /* LN rows per wave iteration       */
+
+    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS];
+    __shared__ int tok[BM];
+    __shared__ int sh_e, sh_row0, sh_rows;
+
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int l16 = lane & 15;
+    const int g = lane >> 4;
+
+    /* ---- schedule ------------------------------------------------------ */
+    const int per_xcd = gridDim.x / 8;
+    const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (wave == 0) {
+        if (a.counts) {
+            const int c = lane < a.n_experts ? min(a.counts[lane], a.cap) : 0;
+            const int nt = (c + BM - 1) / BM;
+            int incl = nt;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            const int excl = incl - nt;
+            const bool mine = lane < a.n_experts && L >= excl && L < incl;
+            const unsigned long long bal = __ballot(mine);
+            if (lane == 0 && bal == 0ull) sh_e = -1;
+            if (mine) {
+                sh_e = lane;
+                sh_row0 = (L - excl) * BM;
+                sh_rows = min(BM, c - (L - excl) * BM);
+            }
+        } else if (lane == 0) {
+            const int row0 = L * BM;
+            sh_e = row0 < a.n_tokens ? 0 : -1;
+            sh_row0 = row0;
+            sh_rows = min(BM, a.n_tokens - row0);
+        }
+    }
+    __syncthreads();
+    const int e = sh_e;
+
+    if (e >= 0) {
+        const int row0 = sh_row0, rows = sh_rows;
+        for (int r = threadIdx.x; r < BM; r += blockDim.x) {
+            int t = -1;
+            if (r < rows) {
+                t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
+                if (t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
+            }
+            tok[r] = t;
+        }
+        __syncthreads();
+
+        /* LN2 of the gathered rows; rows past the segment end are zero */
+#pragma unroll 1
+        for (int it = 0; it < BM / 4 / RPI; ++it) {
+            const int r = wave * (BM / 4) + it * RPI + lane / LPS;
+            const int t = tok[r];
+            ln_row_to_lds<DIM>(a.in + (int64_t)(t >= 0 ? t : 0) * DIM, t >= 0, a.ln_g, a.ln_b, xs + r * LDS);
+        }
+        __syncthreads();
+
+        const uint16_t* w1 = a.w1 + (int64_t)e * DIM * DIM;
+        const uint16_t* w2 = a.w2 + (int64_t)e * DIM * DIM;
+        const float* b1 = a.b1 + (int64_t)e * DIM;
+        const float* b2 = a.b2 + (int64_t)e * DIM;
+
+        f4 acc[RT][TT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[r][t] = f4_zero();
+        /* GEMM1: hidden rows [wave*RT*16, +RT*16) for all BM tokens */
+#pragma unroll 2
+        for (int ks = 0; ks < KS; ++ks) {
+            h8 xf[TT];
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const h8 w = load_frag(w1, (wave * RT + r) * KS + ks, lane);
+#pragma unroll
+                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(w, xf[t], acc[r][t]);
+            }
+        }
+        __syncthreads(); /* every wave is done reading the LN tile */
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int ch = (wave * RT + r) * 16 + 4 * g;
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                h4 gv;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const f16 u = (f16)(acc[r][t][i] + b1[ch + i]);
+                    gv[i] = (f16)gelu_tanh((float)u);
+                }
+                *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = gv;
+                acc[r][t] = f4_zero();
+            }
+        }
+        __syncthreads();
+        /* GEMM2 */
+#pragma unroll 2
+        for (int ks = 0; ks < KS; ++ks) {
+            h8 xf[TT];
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const h8 w = load_frag(w2, (wave * RT + r) * KS + ks, lane);
+#pragma unroll
+                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(w, xf[t], acc[r][t]);
+            }
+        }
+        /* epilogue: bias, fp16 round, + h (fp16 round), scatter to token rows */
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int tk = tok[16 * t + l16];
+            if (tk >= 0) {
+                const int64_t base = (int64_t)tk * DIM;
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    const int ch = (wave * RT + r) * 16 + 4 * g;
+                    const h4 hin = *reinterpret_cast<const h4*>(a.in + base + ch);
+                    h4 y;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const f16 yy = (f16)(acc[r][t][i] + b2[ch + i]);
+                        y[i] = (f16)((float)yy + (float)hin[i]);
+                    }
+                    *reinterpret_cast<h4*>(a.out + base + ch) = y;
+                }
+            }
+        }
+    }
+
+    /* ---- counts ticket --------------------------------------------------- */
+    if (a.counts) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            const int prev = atomicAdd(&a.counts[a.n_experts], 1);
+            if (prev == (int)gridDim.x - 1) {
+                for (int i = 0; i < a.n_experts; ++i) atomicExch(&a.counts[i], 0);
+                atomicExch(&a.counts[a.n_experts], 0);
+                __threadfence();
+            }
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm128(ExpertArgs a) {
+    expert_body<256, 128>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm64(ExpertArgs a) {
+    expert_body<256, 64>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm128(ExpertArgs a) {
+    expert_body<128, 128>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm64(ExpertArgs a) {
+    expert_body<128, 64>(a);
+}
