@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Bench: the MoE-64 bottleneck transformer (d256, 16 blocks, 64 experts, top-1,
+68x120 tokens, Zipf(1.1) routing) on one MI355X.
+
+One step = one pass of the whole 16-block chain over one batch of frames
+(default 16 frames = 130,560 tokens), replayed from the engine's hipGraph.
+Inputs and weights are resident in HBM before timing starts. Prints one JSON
+line (see the keys below); everything else goes to stderr.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 16]
+"""
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "prism-inference_amd"))
+
+import prism_amd as P  # noqa: E402
+
+MFMA_F16_PEAK = 2.5e15   # dense fp16 MFMA, MI355X
+HBM_PEAK = 8.0e12        # HBM3E bytes/s, MI355X
+METRIC = "frames/s + us/frame, MoE-64exp d256x16blk @68x120 tok; % fp16 MFMA peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def attn_flops_per_token(cfg):
+    d = cfg.dim
+    return 2 * (3 * d * d + 2 * 64 * d + d * d)
+
+
+def time_graph(hip, eng, dx, dy, batch, steps, warmup, stream):
+    for _ in range(warmup):
+        eng.forward(dx, dy, batch, stream, graph=True)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        eng.forward(dx, dy, batch, stream, graph=True)
+    hip.record(e1, stream)
+    ms = hip.elapsed_ms(e0, e1)
+    hip.sync()
+    wall = time.perf_counter() - t0
+    return ms / steps, wall
+
+
+def time_stage(hip, launch, reps, stream):
+    """Average duration (ms) of one stage launch, HIP events on its stream."""
+    for _ in range(3):
+        rc = launch()
+        assert rc == 0
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(reps):
+        launch()
+    hip.record(e1, stream)
+    return hip.elapsed_ms(e0, e1) / reps
+
+
+def cpu_baseline(cfg, blob, offs, x_bits, budget_s):
+    """The oracle (fp32 C + OpenMP) on the host cores, one frame at a time."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    w = O.f16bits_to_f32(blob)
+    n = cfg.H * cfg.W
+    x = O.f16bits_to_f32(x_bits[:n * cfg.dim]).reshape(n, cfg.dim)
+    c = O.cfg(cfg.dim, cfg.n_heads, cfg.head_dim, cfg.n_experts, cfg.H, cfg.W, 1, True)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        O.forward(c, w, list(offs), x)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} frame(s) of the same workload at batch 1 (8160 tokens x "
+                      f"{cfg.n_blocks} blocks each), median {med * 1e3:.1f} ms/frame; fp32 oracle "
+                      f"(oracle/oracle.c) with OpenMP, host CPU: {platform.processor() or platform.machine()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--config", default="moe64")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stage-reps", type=int, default=20)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the block chain on one GPU "
+              "(frames and windows shard with no exchange; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = P.CONFIGS[args.config]
+    B = args.batch
+    hip = P.Hip()
+    if hip.device_count() < 1:
+        raise SystemExit("bench.py: no HIP device")
+
+    log(f"[bench] synthesising {cfg.name}: {cfg.n_blocks} blocks, {cfg.n_experts} experts")
+    desc = cfg.desc()
+    blob, offs = P.synth_weights(desc, seed=0, routing=cfg.routing)
+    eng = P.Engine(0)
+    eng.load_weights(desc, blob, offs)
+    T, d = cfg.tokens, cfg.dim
+    x = P.synth_features(cfg, batch=B, seed=1)
+    stream = hip.stream()
+    dx, dy = hip.malloc(B * T * d * 2), hip.malloc(B * T * d * 2)
+    hip.upload(dx, x)
+
+    # ---- batch-B throughput (the step) and batch-1 latency, hipGraph replay
+    log(f"[bench] batch {B}: warmup {args.warmup}, steps {args.steps}")
+    ms_b, wall_b = time_graph(hip, eng, dx, dy, B, args.steps, args.warmup, stream)
+    assign_ptr, ntok = eng.forward_assignments()
+    assign = hip.download(np.empty(cfg.n_blocks * ntok, np.int32), assign_ptr).reshape(cfg.n_blocks, ntok)
+    log(f"[bench] batch 1 latency")
+    ms_1, _ = time_graph(hip, eng, dx, dy, 1, max(args.steps, 50), args.warmup, stream)
+
+    flops_frame = cfg.flops_per_token_block() * T * cfg.n_blocks
+    fps_b = B / (ms_b * 1e-3)
+    weight_bytes = blob.nbytes
+    io_bytes_1 = 2 * T * d * 2
+
+    # ---- per-stage kernel durations (batch B), HIP events on the launch stream
+    n = B * T
+    N = cfg.n_experts
+    feats = hip.malloc(2 * n * d * 2)
+    hip.copy(feats, dx, n * d * 2)
+    aux_n = P.aux_elems(N, n)
+    aux = hip.malloc(aux_n * 4)
+    hip.memset(aux, 0, aux_n * 4)
+    a_push = eng.attn_push(0, 0, n * d)
+    r_push = eng.router_push(0, T, n * d, 0, n, n + N + 1)
+    e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N + 1)
+    log("[bench] per-stage timing")
+    t_attn = time_stage(hip, lambda: eng.attn(a_push, feats, B, stream), args.stage_reps, stream)
+    # router and experts alternate so the counts are consumed between router launches
+    hip.sync()
+    rr = []
+    ee = []
+    for _ in range(args.stage_reps):
+        e0, e1, e2 = hip.event(), hip.event(), hip.event()
+        hip.record(e0, stream)
+        assert eng.router(r_push, feats, aux, B, stream) == 0
+        hip.record(e1, stream)
+        assert eng.experts(e_push, feats, aux, B, stream) == 0
+        hip.record(e2, stream)
+        rr.append(hip.elapsed_ms(e0, e1))
+        ee.append(hip.elapsed_ms(e1, e2))
+    t_router, t_expert = statistics.median(rr), statistics.median(ee)
+    attn_flops = attn_flops_per_token(cfg) * n
+    attn_tflops = attn_flops / (t_attn * 1e-3) / 1e12
+
+    # ---- expert load actually produced (all blocks, batch B)
+    share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
+    hist0 = np.bincount(assign[0], minlength=N)
+
+    out = {
+        "metric": METRIC,
+        "value": round(fps_b, 3),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_b, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, Zipf(1.1)-fitted router bias)",
+        "config": {"workload": f"{cfg.name}: d{d} x {cfg.n_blocks} blocks, 8x32 heads, 8x8 windows, "
+                               f"{N} experts top-1, {cfg.H}x{cfg.W} tokens, batch {B}",
+                   "batch": B, "tokens_per_frame": T, "blocks": cfg.n_blocks, "experts": N,
+                   "parallelism": "single GPU"},
+        "us_per_frame": round(ms_b * 1e3 / B, 3),
+        "mfma_frac": round(flops_frame * B / (ms_b * 1e-3) / MFMA_F16_PEAK, 4),
+        "batch1": {"frames_per_s": round(1e3 / ms_1, 2), "us_per_frame": round(ms_1 * 1e3, 2),
+                   "mfma_frac": round(flops_frame / (ms_1 * 1e-3) / MFMA_F16_PEAK, 4),
+                   "hbm_frac": round((weight_bytes + io_bytes_1) / (ms_1 * 1e-3) / HBM_PEAK, 4)},
+        "stages_ms": {"attention": round(t_attn, 5), "router": round(t_router, 5), "experts": round(t_expert, 5),
+                      "batch": B},
+        "roofline": {"kernel": "prism_attn_d256", "bound": "mfma", "achieved": round(attn_tflops, 2),
+                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": round(attn_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": None,
+                     "flops_per_launch": attn_flops, "avg_launch_ms": round(t_attn, 5)},
+        "expert_load": {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
+                        "hottest_share_mean": round(float(share.mean()), 4),
+                        "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},
+        "wall_s_timed": round(wall_b, 3),
+    }
+    hip.free(feats)
+    hip.free(aux)
+
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline(cfg, blob, offs, x.reshape(-1), args.cpu_budget)
+    else:
+        out["cpu_baseline"] = None
+    hip.free(dx)
+    hip.free(dy)
+    eng.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -51,8 +51,8 @@ struct prism_ctx {
     int device = 0;
     hipModule_t module = nullptr;
     hipFunction_t f_attn[2] = {};       /* [0] d128, [1] d256 */
-    hipFunction_t f_router[2] = {};
-    hipFunction_t f_expert[2][2] = {};  /* [dim][bm64, bm128] */
+    hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
+    hipFunction_t f_expert[2] = {};     /* [dim], 64-token tiles */
     std::string err;
 
     bool loaded = false;
@@ -138,10 +138,12 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         return fail(nullptr, PRISM_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
     }
     struct { hipFunction_t* f; const char* name; } fns[] = {
-        {&c->f_attn[0], "prism_attn_d128"},           {&c->f_attn[1], "prism_attn_d256"},
-        {&c->f_router[0], "prism_router_d128"},       {&c->f_router[1], "prism_router_d256"},
-        {&c->f_expert[0][0], "prism_expert_d128_bm64"}, {&c->f_expert[0][1], "prism_expert_d128_bm128"},
-        {&c->f_expert[1][0], "prism_expert_d256_bm64"}, {&c->f_expert[1][1], "prism_expert_d256_bm128"},
+        {&c->f_attn[0], "prism_attn_d128"},         {&c->f_attn[1], "prism_attn_d256"},
+        {&c->f_router[0][0], "prism_router_d128_n1"}, {&c->f_router[0][1], "prism_router_d128_n2"},
+        {&c->f_router[0][2], "prism_router_d128_n3"}, {&c->f_router[0][3], "prism_router_d128_n4"},
+        {&c->f_router[1][0], "prism_router_d256_n1"}, {&c->f_router[1][1], "prism_router_d256_n2"},
+        {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
+        {&c->f_expert[0], "prism_expert_d128_bm64"},  {&c->f_expert[1], "prism_expert_d256_bm64"},
     };
     for (auto& f : fns) {
         e = hipModuleGetFunction(f.f, c->module, f.name);
@@ -396,7 +398,7 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
     a.np = round16(N);
     a.cap = (int32_t)n;
     const int64_t grid = (n + 127) / 128;
-    return launch(c, c->f_router[dim_index(c->desc.dim)], (unsigned)grid, a, s);
+    return launch(c, c->f_router[dim_index(c->desc.dim)][a.np / 16 - 1], (unsigned)grid, a, s);
 }
 
 int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int32_t* counts,
@@ -416,11 +418,10 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     a.n_tokens = (int32_t)n;
     a.n_experts = N;
     a.cap = (int32_t)n;
-    const int bm_idx = n >= 65536 ? 1 : 0;
-    const int64_t bm = bm_idx ? 128 : 64;
+    const int64_t bm = 64;
     int64_t tiles = (n + bm - 1) / bm + (counts ? N : 0);
     tiles = (tiles + 7) / 8 * 8;
-    return launch(c, c->f_expert[dim_index(D)][bm_idx], (unsigned)tiles, a, s);
+    return launch(c, c->f_expert[dim_index(D)], (unsigned)tiles, a, s);
 }
 
 /* which: 0 = attention (qkv_w), 1 = router (router_w), 2 = experts (exp_w1) */

@@ -18,28 +18,66 @@
  *     O^T is normalised, rounded to fp16 and written to os (LDS).
  *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x (fp16 round), store.
  *
- * Weights (packed fragments) are read straight from global memory; all
- * workgroups read the same 0.5 MiB per block, which stays L2-resident.
+ * Weight streaming: every wave reads one fixed sequence of 1 KiB weight
+ * fragments (head A's QKV k-steps, head B's, then the out-proj's) through a
+ * register ring PF fragments deep, so loads run 2 k-steps ahead of the MFMAs
+ * and the next head's and the out-proj's first fragments are in flight while
+ * the softmax math runs. All workgroups read the same 0.5 MiB per block,
+ * which stays L2-resident. Biases and LN parameters are staged in LDS once.
  */
 #pragma once
 #include "common.hpp"
 
 template <int DIM, int HD>
+struct AttnShape {
+    static constexpr int KS = DIM / 32;            /* k-steps over the model dim     */
+    static constexpr int CT = HD / 16;             /* 16-channel tiles per head      */
+    static constexpr int FPK = 3 * CT;             /* QKV fragments per k-step       */
+    static constexpr int HEADF = KS * FPK;         /* fragments per head             */
+    static constexpr int ORT = DIM / 64;           /* out-proj row tiles per wave    */
+    static constexpr int OUTF = KS * ORT;          /* out-proj fragments             */
+    static constexpr int TOTAL = 2 * HEADF + OUTF; /* fragment sequence length       */
+    static constexpr int PF = 2 * FPK;             /* ring depth (2 k-steps ahead)   */
+    static constexpr int LDS = DIM + 8;            /* padded LDS row, halfs          */
+};
+
+/* Fragment p of wave `wave`'s sequence: head A's QKV k-steps, head B's, then
+ * the out-proj's (p is a compile-time constant or depends only on the head
+ * index, so both branches are wave-uniform). */
+template <int DIM, int HD>
+__device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, int wave, int p, int loff) {
+    using S = AttnShape<DIM, HD>;
+    if (p < 2 * S::HEADF) {
+        const int hh = p / S::HEADF, q = p % S::HEADF;
+        const int ks = q / S::FPK, f = q % S::FPK;
+        const int mat = f / S::CT, c = f % S::CT; /* 0 = Q, 1 = K, 2 = V */
+        const int h = wave + 4 * hh;
+        const int rt = (mat * DIM + h * HD) / 16 + c;
+        return wqkv.load(rt * S::KS + ks, loff);
+    }
+    const int q = p - 2 * S::HEADF;
+    const int ks = q / S::ORT, r = q % S::ORT;
+    return wo.load((wave * S::ORT + r) * S::KS + ks, loff);
+}
+
+template <int DIM, int HD>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     static_assert(DIM / HD == 8, "8 heads");
-    constexpr int KS = DIM / 32;        /* k-steps over the model dim      */
-    constexpr int CT = HD / 16;         /* 16-channel tiles per head       */
-    constexpr int LDS = DIM + 8;        /* padded LDS row, halfs           */
-    constexpr int ORT = DIM / 64;       /* out-proj row tiles per wave     */
+    using S = AttnShape<DIM, HD>;
+    constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT, PF = S::PF;
     constexpr float LOG2E = 1.4426950408889634f;
     const float scale = (HD == 32) ? 0.1767766953f : 1.0f / sqrtf((float)HD);
     const float sl2 = scale * LOG2E;
 
     __shared__ __attribute__((aligned(16))) f16 xs[64 * LDS];
     __shared__ __attribute__((aligned(16))) f16 os[64 * LDS];
+    __shared__ float s_bqkv[3 * DIM];
+    __shared__ float s_bo[DIM];
+    __shared__ float s_g[DIM];
+    __shared__ float s_b[DIM];
 
     const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
 
@@ -51,114 +89,142 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     const uint16_t* in = a.in + (int64_t)frame * a.frame_elems;
     uint16_t* out = a.out + (int64_t)frame * a.frame_elems;
 
-    /* ---- 1. LN1 ------------------------------------------------------ */
+    const FragSrc src_qkv(a.wqkv, 3u * DIM * DIM * 2u);
+    const FragSrc src_o(a.wo, 1u * DIM * DIM * 2u);
+    const int loff = lane * 16;
+
+    /* weight ring: first PF fragments go out before anything else */
+    h8 ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p, loff);
+    sched_fence();
+
+    for (int i = threadIdx.x; i < 3 * DIM; i += 256) s_bqkv[i] = a.bqkv[i];
+    for (int i = threadIdx.x; i < DIM; i += 256) {
+        s_bo[i] = a.bo[i];
+        s_g[i] = a.ln_g[i];
+        s_b[i] = a.ln_b[i];
+    }
+
+    /* ---- 1. LN1: all row loads first, then the math ------------------ */
     {
         constexpr int LPS = DIM / 16;
         constexpr int SPI = 64 / LPS; /* slots per wave iteration */
+        constexpr int IT = 16 / SPI;
+        RowChunk rc[IT];
+        bool valid[IT];
 #pragma unroll
-        for (int it = 0; it < 16 / SPI; ++it) {
+        for (int it = 0; it < IT; ++it) {
             const int s = wave * 16 + it * SPI + lane / LPS;
             const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-            const bool valid = gy < a.H && gx < a.W;
-            const int t = valid ? gy * a.W + gx : 0;
-            ln_row_to_lds<DIM>(in + (int64_t)t * DIM, valid, a.ln_g, a.ln_b, xs + s * LDS);
+            valid[it] = gy < a.H && gx < a.W;
+            rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
         }
+        __syncthreads(); /* LN parameters staged */
+#pragma unroll
+        for (int it = 0; it < IT; ++it)
+            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * 16 + it * SPI + lane / LPS) * LDS, nullptr);
     }
     __syncthreads();
 
     /* ---- 2./3. per head ----------------------------------------------- */
+    static_assert(S::HEADF % PF == 0, "ring slots must not depend on the head index");
 #pragma unroll 1
     for (int hh = 0; hh < 2; ++hh) {
+        /* keeps the head-invariant xs reads inside the loop (hoisting all of
+         * them out would pin 32 fragments in registers) */
+        asm volatile("" ::: "memory");
         const int h = wave + 4 * hh;
+        /* accumulators start at the bias, so the MFMAs add it.
+         * Q^T/K^T element i: channel 16c+4g+i, token 16t+l16.
+         * V element i: token 16t+4g+i, channel 16c+l16. */
         f4 accQ[CT][4], accK[CT][4], accV[4][CT];
 #pragma unroll
-        for (int c = 0; c < CT; ++c)
+        for (int c = 0; c < CT; ++c) {
+            const int chq = h * HD + 16 * c + 4 * g;
+            const f4 bq = {s_bqkv[chq], s_bqkv[chq + 1], s_bqkv[chq + 2], s_bqkv[chq + 3]};
+            const f4 bk = {s_bqkv[DIM + chq], s_bqkv[DIM + chq + 1], s_bqkv[DIM + chq + 2], s_bqkv[DIM + chq + 3]};
+            const float bv = s_bqkv[2 * DIM + h * HD + 16 * c + l16];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) { accQ[c][t] = f4_zero(); accK[c][t] = f4_zero(); accV[t][c] = f4_zero(); }
+            for (int t = 0; t < 4; ++t) { accQ[c][t] = bq; accK[c][t] = bk; accV[t][c] = f4{bv, bv, bv, bv}; }
+        }
 
-        const int rtq = (h * HD) / 16;
-        const int rtk = (DIM + h * HD) / 16;
-        const int rtv = (2 * DIM + h * HD) / 16;
-#pragma unroll 2
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             h8 xf[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
-            for (int c = 0; c < CT; ++c) {
-                const h8 wq = load_frag(a.wqkv, (rtq + c) * KS + ks, lane);
-                const h8 wk = load_frag(a.wqkv, (rtk + c) * KS + ks, lane);
-                const h8 wv = load_frag(a.wqkv, (rtv + c) * KS + ks, lane);
+            for (int f = 0; f < S::FPK; ++f) {
+                const int p = hh * S::HEADF + ks * S::FPK + f;
+                const h8 w = ring[p % PF];
+                const int mat = f / CT, c = f % CT;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    accQ[c][t] = mfma_16x16x32(wq, xf[t], accQ[c][t]);
-                    accK[c][t] = mfma_16x16x32(wk, xf[t], accK[c][t]);
-                    accV[t][c] = mfma_16x16x32(xf[t], wv, accV[t][c]);
+                    if (mat == 0) accQ[c][t] = mfma_16x16x32(w, xf[t], accQ[c][t]);
+                    else if (mat == 1) accK[c][t] = mfma_16x16x32(w, xf[t], accK[c][t]);
+                    else accV[t][c] = mfma_16x16x32(xf[t], w, accV[t][c]);
                 }
+                ring[p % PF] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p + PF, loff); /* p + PF < TOTAL here */
             }
+            sched_fence();
         }
 
-        /* bias + fp16 round. Q^T/K^T element i: channel 16c+4g+i, token 16t+l16.
-         * V element i: token 16t+4g+i, channel 16c+l16. */
+        /* fp16 round (the bias is already in) */
         h4 q4[CT][4], k4[CT][4], v4[4][CT];
 #pragma unroll
-        for (int c = 0; c < CT; ++c) {
-            const int chq = h * HD + 16 * c + 4 * g;
-            const int chv = 2 * DIM + h * HD + 16 * c + l16;
-            const float bv = a.bqkv[chv];
+        for (int c = 0; c < CT; ++c)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    q4[c][t][i] = (f16)(accQ[c][t][i] + a.bqkv[chq + i]);
-                    k4[c][t][i] = (f16)(accK[c][t][i] + a.bqkv[DIM + chq + i]);
-                    v4[t][c][i] = (f16)(accV[t][c][i] + bv);
-                }
+                q4[c][t] = cvt_h4(accQ[c][t]);
+                k4[c][t] = cvt_h4(accK[c][t]);
+                v4[t][c] = cvt_h4(accV[t][c]);
             }
-        }
 
-        /* S^T[key tile kt][query tile qt]: element i = key 16kt+4g+i, query 16qt+l16 */
-        f4 s[4][4];
+        /* Per query tile qt: S^T[kt] (element i = key 16kt+4g+i, query 16qt+l16),
+         * softmax down the key axis (16 values in-lane, then the 4 lane groups),
+         * P kept as fp16 operands for the P.V MFMA. */
+        h4 p[4][4];
+        float inv[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int qt = 0; qt < 4; ++qt) {
+            f4 s[4];
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt) {
+            for (int kt = 0; kt < 4; ++kt) {
                 if constexpr (CT == 2) {
                     const h8 ka = {k4[0][kt][0], k4[0][kt][1], k4[0][kt][2], k4[0][kt][3],
                                    k4[1][kt][0], k4[1][kt][1], k4[1][kt][2], k4[1][kt][3]};
                     const h8 qb = {q4[0][qt][0], q4[0][qt][1], q4[0][qt][2], q4[0][qt][3],
                                    q4[1][qt][0], q4[1][qt][1], q4[1][qt][2], q4[1][qt][3]};
-                    s[kt][qt] = mfma_16x16x32(ka, qb, f4_zero());
+                    s[kt] = mfma_16x16x32(ka, qb, f4_zero());
                 } else {
-                    s[kt][qt] = mfma_16x16x16(k4[0][kt], q4[0][qt], f4_zero());
+                    s[kt] = mfma_16x16x16(k4[0][kt], q4[0][qt], f4_zero());
                 }
             }
-
-        /* softmax down the key axis for each query column */
-        h4 p[4][4];
-        float inv[4];
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
             float m = -3.0e38f;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
+                for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kt][i]);
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
+            /* exp(scale * (s - m)) = 2^(s * sl2 - m * sl2) */
+            const float msl = m * sl2;
             float sum = 0.f;
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < 4; ++kt) {
+                f4 e;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = exp2f((s[kt][qt][i] - m) * sl2);
-                    sum += e;
-                    p[kt][qt][i] = (f16)e;
+                    e[i] = fast_exp2(__builtin_fmaf(s[kt][i], sl2, -msl));
+                    sum += e[i];
                 }
+                p[kt][qt] = cvt_h4(e);
+            }
             sum += __shfl_xor(sum, 16, 64);
             sum += __shfl_xor(sum, 32, 64);
-            inv[qt] = 1.0f / fmaxf(sum, 1e-6f);
+            inv[qt] = fast_rcp(fmaxf(sum, 1e-6f));
         }
 
         /* O^T[channel tile dt][query tile qt] = V^T P^T over 64 keys (2 k-steps) */
@@ -177,21 +243,37 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                                    p[2 * st + 1][qt][3]};
                     o = mfma_16x16x32(va, pb, o);
                 }
-                h4 r;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv[qt]);
+                const h4 r = cvt_h4(o * inv[qt]);
                 *reinterpret_cast<h4*>(os + (16 * qt + l16) * LDS + h * HD + 16 * dt + 4 * g) = r;
             }
+    }
+
+    /* residual rows for the epilogue, fetched while the out-proj runs */
+    h4 xin[4][ORT];
+    bool vt[4];
+    int64_t tbase[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int s = 16 * t + l16;
+        const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
+        vt[t] = gy < a.H && gx < a.W;
+        tbase[t] = (int64_t)(vt[t] ? gy * a.W + gx : 0) * DIM;
+#pragma unroll
+        for (int r = 0; r < ORT; ++r)
+            xin[t][r] = *reinterpret_cast<const h4*>(in + tbase[t] + (wave * ORT + r) * 16 + 4 * g);
     }
     __syncthreads();
 
     /* ---- 4. out-proj + residual --------------------------------------- */
-    f4 acc[ORT][4];
+    f4 acc[ORT][4]; /* starts at the out-proj bias */
 #pragma unroll
-    for (int r = 0; r < ORT; ++r)
+    for (int r = 0; r < ORT; ++r) {
+        const int ch = (wave * ORT + r) * 16 + 4 * g;
+        const f4 bo = {s_bo[ch], s_bo[ch + 1], s_bo[ch + 2], s_bo[ch + 3]};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[r][t] = f4_zero();
-#pragma unroll 2
+        for (int t = 0; t < 4; ++t) acc[r][t] = bo;
+    }
+#pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         h8 of[4];
 #pragma unroll
@@ -199,28 +281,22 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             of[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
-            const h8 w = load_frag(a.wo, (wave * ORT + r) * KS + ks, lane);
+            const int p = 2 * S::HEADF + ks * ORT + r;
+            const h8 w = ring[p % PF];
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
+            if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p + PF, loff);
         }
+        sched_fence();
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const int s = 16 * t + l16;
-        const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-        if (gy < a.H && gx < a.W) {
-            const int64_t base = (int64_t)(gy * a.W + gx) * DIM;
+        if (vt[t]) {
 #pragma unroll
             for (int r = 0; r < ORT; ++r) {
                 const int ch = (wave * ORT + r) * 16 + 4 * g;
-                const h4 xin = *reinterpret_cast<const h4*>(in + base + ch);
-                h4 y;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const f16 po = (f16)(acc[r][t][i] + a.bo[ch + i]);
-                    y[i] = (f16)((float)po + (float)xin[i]);
-                }
-                *reinterpret_cast<h4*>(out + base + ch) = y;
+                /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding) */
+                *reinterpret_cast<h4*>(out + tbase[t] + ch) = add_f16x4(cvt_h4(acc[r][t]), xin[t][r]);
             }
         }
     }

@@ -31,6 +31,11 @@ __device__ __forceinline__ f4 mfma_16x16x16(h4 a, h4 b, f4 c) {
 
 __device__ __forceinline__ f4 f4_zero() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
+/* Stops the machine scheduler from moving any instruction across this point.
+ * Used at k-step boundaries so prefetch loads stay where they are issued
+ * instead of being sunk next to their first use. */
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
 /* Sum over groups of `width` consecutive lanes (width a power of two <= 64). */
@@ -46,33 +51,99 @@ __device__ __forceinline__ h8 load_frag(const uint16_t* packed, int frag, int la
     return reinterpret_cast<const h8*>(packed)[frag * 64 + lane];
 }
 
+/*
+ * Packed weight matrix read through a buffer resource: the base and size sit
+ * in SGPRs, the fragment offset (frag * 1 KiB, wave-uniform) in an SGPR and
+ * the lane offset (lane * 16 B) in one shared VGPR, so a wave can keep dozens
+ * of fragment loads in flight without spending VGPRs on addresses. Offsets at
+ * or past `bytes` read as zero instead of faulting.
+ */
+struct FragSrc {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ __forceinline__ FragSrc(const uint16_t* base, uint32_t bytes)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000)) {}
+    __device__ __forceinline__ h8 load(int frag, int lane_off) const {
+        return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, frag * 1024, 0));
+    }
+};
+
+/* 2^x on the hardware transcendental unit (v_exp_f32). */
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+/* 1/x on the hardware reciprocal unit (v_rcp_f32, 1 ulp). */
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
 /* GELU-tanh, 0.5u(1 + tanh(0.7978846(u + 0.044715u^3))), evaluated through the
- * identity 0.5(1 + tanh(z)) = 1/(1 + exp(-2z)). */
+ * identity 0.5(1 + tanh(z)) = 1/(1 + exp(-2z)) = 1/(1 + 2^(-2z log2 e)).
+ * Large negative u gives 2^+inf = inf and u * 0 = -0; large positive u gives
+ * u * 1. */
 __device__ __forceinline__ float gelu_tanh(float u) {
-    const float z = 0.7978846f * (u + 0.044715f * u * u * u);
-    return u / (1.0f + __expf(-2.0f * z));
+    constexpr float K = -2.0f * 0.7978846f * 1.4426950408889634f;
+    const float inner = __builtin_fmaf(0.044715f * u * u, u, u);
+    return u * fast_rcp(1.0f + fast_exp2(inner * K));
+}
+
+/*
+ * Every fp32 -> fp16 rounding point goes through `opaque` first: the value is
+ * pinned in fp32 registers, so the compiler cannot fold the producing
+ * multiply/FMA and the conversion into one v_fma_mix*_f16 (a single rounding
+ * straight to fp16). That fold is applied to some unrolled copies and not
+ * others, which would make a token's result depend on its row in a tile.
+ * The asm emits no instruction.
+ */
+template <class T>
+__device__ __forceinline__ T opaque(T v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+/* fp16 a + b with one rounding: the reference's fp16 residual add. */
+__device__ __forceinline__ h4 add_f16x4(h4 a, h4 b) { return opaque(a) + opaque(b); }
+
+/* Packed conversion of 4 fp32 values to fp16 (round to nearest even). */
+__device__ __forceinline__ h4 cvt_h4(f4 v) {
+    v = opaque(v);
+    return h4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
 }
 
 /*
  * LayerNorm of rows into an LDS tile, LPS = DIM/16 lanes per row and 16
- * channels per lane. Rows whose `valid` flag is false are written as zeros.
- * Two-pass mean / biased variance in fp32; output rounded to fp16.
+ * channels per lane, in two steps so a kernel can put every row load in
+ * flight before it does any math: ln_load fetches the lane's 16 halfs of a
+ * row (zeros for an invalid row), ln_store normalises them into `dst` (and
+ * copies the raw values to `raw_dst` if given). Two-pass mean / biased
+ * variance in fp32; output rounded to fp16; invalid rows are written as
+ * zeros. g and b live in LDS.
  */
+struct RowChunk {
+    h8 a0, a1;
+};
+
 template <int DIM>
-__device__ __forceinline__ void ln_row_to_lds(const uint16_t* row, bool valid, const float* g,
-                                              const float* b, f16* dst) {
+__device__ __forceinline__ RowChunk ln_load(const uint16_t* row, bool valid) {
     constexpr int LPS = DIM / 16;
     const int c0 = (lane_id() % LPS) * 16;
-    float v[16];
+    RowChunk r{h8{}, h8{}};
     if (valid) {
         const h8* p = reinterpret_cast<const h8*>(row + c0);
-        const h8 a0 = p[0], a1 = p[1];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) { v[j] = (float)a0[j]; v[8 + j] = (float)a1[j]; }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = 0.f;
+        r.a0 = p[0];
+        r.a1 = p[1];
     }
+    return r;
+}
+
+template <int DIM>
+__device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const float* g, const float* b,
+                                         f16* dst, f16* raw_dst) {
+    constexpr int LPS = DIM / 16;
+    const int c0 = (lane_id() % LPS) * 16;
+    if (raw_dst) {
+        h8* rd = reinterpret_cast<h8*>(raw_dst + c0);
+        rd[0] = rc.a0;
+        rd[1] = rc.a1;
+    }
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { v[j] = (float)rc.a0[j]; v[8 + j] = (float)rc.a1[j]; }
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) s += v[j];
@@ -80,16 +151,37 @@ __device__ __forceinline__ void ln_row_to_lds(const uint16_t* row, bool valid, c
     const float mean = s * (1.0f / DIM);
     float q = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) { const float t = v[j] - mean; q += t * t; }
+    for (int j = 0; j < 16; ++j) {
+        v[j] -= mean;
+        q = __builtin_fmaf(v[j], v[j], q);
+    }
     q = group_sum<LPS>(q);
     const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
     h8 o0, o1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        o0[j] = valid ? (f16)((v[j] - mean) * inv * g[c0 + j] + b[c0 + j]) : (f16)0.f;
-        o1[j] = valid ? (f16)((v[8 + j] - mean) * inv * g[c0 + 8 + j] + b[c0 + 8 + j]) : (f16)0.f;
+    for (int j = 0; j < 8; j += 4) {
+        const f4 n0 = {__builtin_fmaf(v[j], inv * g[c0 + j], b[c0 + j]),
+                       __builtin_fmaf(v[j + 1], inv * g[c0 + j + 1], b[c0 + j + 1]),
+                       __builtin_fmaf(v[j + 2], inv * g[c0 + j + 2], b[c0 + j + 2]),
+                       __builtin_fmaf(v[j + 3], inv * g[c0 + j + 3], b[c0 + j + 3])};
+        const f4 n1 = {__builtin_fmaf(v[8 + j], inv * g[c0 + 8 + j], b[c0 + 8 + j]),
+                       __builtin_fmaf(v[9 + j], inv * g[c0 + 9 + j], b[c0 + 9 + j]),
+                       __builtin_fmaf(v[10 + j], inv * g[c0 + 10 + j], b[c0 + 10 + j]),
+                       __builtin_fmaf(v[11 + j], inv * g[c0 + 11 + j], b[c0 + 11 + j])};
+        const h4 p0 = cvt_h4(n0), p1 = cvt_h4(n1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o0[j + i] = p0[i];
+            o1[j + i] = p1[i];
+        }
     }
+    /* padded / missing rows are zero: select on whole 32-bit words */
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 w0 = __builtin_bit_cast(u4, o0), w1 = __builtin_bit_cast(u4, o1);
+    const unsigned int keep = valid ? 0xffffffffu : 0u;
+    w0 &= keep;
+    w1 &= keep;
     h8* d = reinterpret_cast<h8*>(dst + c0);
-    d[0] = o0;
-    d[1] = o1;
+    d[0] = __builtin_bit_cast(h8, w0);
+    d[1] = __builtin_bit_cast(h8, w1);
 }

@@ -16,13 +16,21 @@
  * per-expert counts into a tile prefix sum and finds its (expert, row block);
  * tiles past the end do nothing.
  *
+ * Weight streaming: as soon as the tokens are gathered, each wave issues
+ * every W1 fragment of its 16*RT output rows (RT*KS 1 KiB fragments, held in
+ * registers) right behind the row loads, so W1 arrives while LN2 runs. GEMM1
+ * refills the registers of its first KS/2 k-steps with the first half of W2
+ * (in flight during GEMM1 and the GELU); GEMM2 issues the second half of W2
+ * while it consumes the first.
+ *
  * Counts ticket: every workgroup, active or not, takes a ticket at the end;
  * the last one returns counts[0..N] to zero for the next router launch.
  *
  * GEMMs are C^T = W * A^T (weights as the A operand, tokens as columns), so a
  * lane's accumulator holds 4 consecutive channels of one token: 8-byte LDS
  * writes for the GELU tile and 8-byte global stores for the output rows,
- * scattered straight back to the token's HWC position (fused unpermute).
+ * scattered straight back to the token's HWC position (fused unpermute). The
+ * raw rows stay in LDS for the residual.
  */
 #pragma once
 #include "common.hpp"
@@ -36,12 +44,14 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     constexpr int LPS = DIM / 16; /* LN lanes per row                 */
     constexpr int RPI = 64 / LPS; /* LN rows per wave iteration       */
 
-    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS];
+    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, then GELU output */
+    __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
+    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
     __shared__ int tok[BM];
     __shared__ int sh_e, sh_row0, sh_rows;
 
     const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
 
@@ -73,13 +83,26 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             sh_row0 = row0;
             sh_rows = min(BM, a.n_tokens - row0);
         }
+    } else {
+        for (int i = threadIdx.x - 64; i < DIM; i += 192) {
+            s_g[i] = a.ln_g[i];
+            s_b[i] = a.ln_b[i];
+        }
     }
     __syncthreads();
-    const int e = sh_e;
+    const int e = __builtin_amdgcn_readfirstlane(sh_e);
 
     if (e >= 0) {
         const int row0 = sh_row0, rows = sh_rows;
-        for (int r = threadIdx.x; r < BM; r += blockDim.x) {
+        const FragSrc w1(a.w1 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
+        const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
+        const int loff = lane * 16;
+
+        for (int i = threadIdx.x; i < DIM; i += 256) {
+            s_b1[i] = a.b1[(int64_t)e * DIM + i];
+            s_b2[i] = a.b2[(int64_t)e * DIM + i];
+        }
+        for (int r = threadIdx.x; r < BM; r += 256) {
             int t = -1;
             if (r < rows) {
                 t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
@@ -89,27 +112,40 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         }
         __syncthreads();
 
-        /* LN2 of the gathered rows; rows past the segment end are zero */
-#pragma unroll 1
-        for (int it = 0; it < BM / 4 / RPI; ++it) {
+        /* the gathered rows' loads go out first, then every W1 fragment of
+         * this wave's rows, then LN2 runs on the rows while W1 arrives
+         * (loads retire in issue order) */
+        constexpr int IT = BM / 4 / RPI;
+        RowChunk rc[IT];
+        int rt_tok[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            rt_tok[it] = tok[wave * (BM / 4) + it * RPI + lane / LPS];
+            rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM, rt_tok[it] >= 0);
+        }
+        h8 wf[RT][KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int r = 0; r < RT; ++r) wf[r][ks] = w1.load((wave * RT + r) * KS + ks, loff);
+        sched_fence();
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
             const int r = wave * (BM / 4) + it * RPI + lane / LPS;
-            const int t = tok[r];
-            ln_row_to_lds<DIM>(a.in + (int64_t)(t >= 0 ? t : 0) * DIM, t >= 0, a.ln_g, a.ln_b, xs + r * LDS);
+            ln_store<DIM>(rc[it], rt_tok[it] >= 0, s_g, s_b, xs + r * LDS, hs + r * LDS);
         }
         __syncthreads();
 
-        const uint16_t* w1 = a.w1 + (int64_t)e * DIM * DIM;
-        const uint16_t* w2 = a.w2 + (int64_t)e * DIM * DIM;
-        const float* b1 = a.b1 + (int64_t)e * DIM;
-        const float* b2 = a.b2 + (int64_t)e * DIM;
-
-        f4 acc[RT][TT];
+        f4 acc[RT][TT]; /* starts at b1 */
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
+        for (int r = 0; r < RT; ++r) {
+            const int ch = (wave * RT + r) * 16 + 4 * g;
+            const f4 bb = {s_b1[ch], s_b1[ch + 1], s_b1[ch + 2], s_b1[ch + 3]};
 #pragma unroll
-            for (int t = 0; t < TT; ++t) acc[r][t] = f4_zero();
+            for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+        }
         /* GEMM1: hidden rows [wave*RT*16, +RT*16) for all BM tokens */
-#pragma unroll 2
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             h8 xf[TT];
 #pragma unroll
@@ -117,30 +153,30 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
                 xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const h8 w = load_frag(w1, (wave * RT + r) * KS + ks, lane);
 #pragma unroll
-                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(w, xf[t], acc[r][t]);
+                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
+                if (ks < KS / 2) wf[r][ks] = w2.load((wave * RT + r) * KS + ks, loff);
             }
+            sched_fence();
         }
         __syncthreads(); /* every wave is done reading the LN tile */
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             const int ch = (wave * RT + r) * 16 + 4 * g;
+            const f4 bb = {s_b2[ch], s_b2[ch + 1], s_b2[ch + 2], s_b2[ch + 3]};
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
-                h4 gv;
+                const h4 u = cvt_h4(acc[r][t]); /* r16(W1 hn + b1) */
+                f4 gl;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const f16 u = (f16)(acc[r][t][i] + b1[ch + i]);
-                    gv[i] = (f16)gelu_tanh((float)u);
-                }
-                *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = gv;
-                acc[r][t] = f4_zero();
+                for (int i = 0; i < 4; ++i) gl[i] = gelu_tanh((float)u[i]);
+                *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = cvt_h4(gl);
+                acc[r][t] = bb; /* GEMM2 starts at b2 */
             }
         }
         __syncthreads();
         /* GEMM2 */
-#pragma unroll 2
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             h8 xf[TT];
 #pragma unroll
@@ -148,10 +184,12 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
                 xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const h8 w = load_frag(w2, (wave * RT + r) * KS + ks, lane);
 #pragma unroll
-                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(w, xf[t], acc[r][t]);
+                for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
+                /* second half of W2, issued one half ahead of its use */
+                if (ks < KS / 2) wf[r][ks + KS / 2] = w2.load((wave * RT + r) * KS + ks + KS / 2, loff);
             }
+            sched_fence();
         }
         /* epilogue: bias, fp16 round, + h (fp16 round), scatter to token rows */
 #pragma unroll
@@ -162,14 +200,9 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
                 for (int r = 0; r < RT; ++r) {
                     const int ch = (wave * RT + r) * 16 + 4 * g;
-                    const h4 hin = *reinterpret_cast<const h4*>(a.in + base + ch);
-                    h4 y;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const f16 yy = (f16)(acc[r][t][i] + b2[ch + i]);
-                        y[i] = (f16)((float)yy + (float)hin[i]);
-                    }
-                    *reinterpret_cast<h4*>(a.out + base + ch) = y;
+                    const h4 hin = *reinterpret_cast<const h4*>(hs + (16 * t + l16) * LDS + ch);
+                    /* y = r16(W2 g + b2); out = y + h in fp16 (one rounding) */
+                    *reinterpret_cast<h4*>(a.out + base + ch) = add_f16x4(cvt_h4(acc[r][t]), hin);
                 }
             }
         }
@@ -190,14 +223,8 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm128(ExpertArgs a) {
-    expert_body<256, 128>(a);
-}
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm64(ExpertArgs a) {
     expert_body<256, 64>(a);
-}
-extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm128(ExpertArgs a) {
-    expert_body<128, 128>(a);
 }
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm64(ExpertArgs a) {
     expert_body<128, 64>(a);

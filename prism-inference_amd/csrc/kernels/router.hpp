@@ -13,46 +13,65 @@
  * Workgroup = 4 waves x 32 tokens. A lane owns one token of a 16-token tile
  * and the 8-channel slices 32*ks + 8*g .. +7 of it, which is exactly the
  * B-operand fragment of logits^T = W_r * hn^T, so LN2 runs in registers.
+ * NPT = padded experts / 16 is a template parameter; the workgroup copies
+ * the NPT*KS router fragments into LDS once and every wave reads them from
+ * there, which keeps the register count low enough for several workgroups
+ * per CU.
  */
 #pragma once
 #include "common.hpp"
 
 #define ROUTER_TOKENS_PER_WG 128
 
-template <int DIM>
+template <int DIM, int NPT>
 __device__ __forceinline__ void router_body(const RouterArgs& a) {
     constexpr int KS = DIM / 32;
-    constexpr int TT = 2; /* token tiles per wave */
+    constexpr int TT = 2;            /* token tiles per wave */
+    constexpr int NF = NPT * KS;     /* router fragments     */
     __shared__ int hist[64];
     __shared__ int base[64];
+    __shared__ float s_g[DIM], s_b[DIM], s_br[16 * NPT];
+    __shared__ __attribute__((aligned(16))) h8 s_wr[NF * 64]; /* fragment-ordered W_r */
 
     const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
+
+    /* this wave's token rows first, then the cooperative W_r copy */
+    const int tok0 = blockIdx.x * ROUTER_TOKENS_PER_WG + wave * 16 * TT;
+    h8 xr[TT][KS];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        const int token = tok0 + 16 * tt + l16;
+        const uint16_t* row = a.in + (int64_t)(token < a.n_tokens ? token : 0) * DIM;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            xr[tt][ks] = token < a.n_tokens ? *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g) : h8{};
+    }
+    {
+        const FragSrc src_r(a.wr, 16u * NPT * DIM * 2u);
+        for (int i = threadIdx.x; i < NF * 64; i += 256) s_wr[i] = src_r.load(i / 64, (i % 64) * 16);
+    }
     if (threadIdx.x < 64) hist[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < DIM; i += 256) {
+        s_g[i] = a.ln_g[i];
+        s_b[i] = a.ln_b[i];
+    }
+    for (int i = threadIdx.x; i < 16 * NPT; i += 256) s_br[i] = a.br[i];
     __syncthreads();
 
-    const int tok0 = blockIdx.x * ROUTER_TOKENS_PER_WG + wave * 16 * TT;
     int my_e[TT], my_rank[TT];
-
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
         const int token = tok0 + 16 * tt + l16;
         const bool valid = token < a.n_tokens;
-        float x[KS][8];
-        const uint16_t* row = a.in + (int64_t)(valid ? token : 0) * DIM;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const h8 v = valid ? *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g) : h8{};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[ks][j] = (float)v[j];
-        }
+        /* LN2 in registers: this lane holds channels 32ks + 8g + j */
         float s = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s += x[ks][j];
+            for (int j = 0; j < 8; ++j) s += (float)xr[tt][ks][j];
         s += __shfl_xor(s, 16, 64);
         s += __shfl_xor(s, 32, 64);
         const float mean = s * (1.0f / DIM);
@@ -60,31 +79,48 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) { const float t = x[ks][j] - mean; q += t * t; }
+            for (int j = 0; j < 8; ++j) {
+                const float t = (float)xr[tt][ks][j] - mean;
+                q = __builtin_fmaf(t, t, q);
+            }
         q += __shfl_xor(q, 16, 64);
         q += __shfl_xor(q, 32, 64);
         const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
-        h8 hn[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = 32 * ks + 8 * g + j;
-                hn[ks][j] = (f16)((x[ks][j] - mean) * inv * a.ln_g[c] + a.ln_b[c]);
-            }
 
         /* logits^T: element i of row tile rt = expert 16rt+4g+i, token l16 */
+        f4 acc[NPT];
+#pragma unroll
+        for (int rt = 0; rt < NPT; ++rt)
+            acc[rt] = f4{s_br[16 * rt + 4 * g], s_br[16 * rt + 4 * g + 1], s_br[16 * rt + 4 * g + 2],
+                         s_br[16 * rt + 4 * g + 3]};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            asm volatile("" ::: "memory"); /* keep this k-step's gamma/beta reads here */
+            h8 hn;
+#pragma unroll
+            for (int j = 0; j < 8; j += 4) {
+                f4 t;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int c = 32 * ks + 8 * g + j + i;
+                    t[i] = __builtin_fmaf((float)xr[tt][ks][j + i] - mean, inv * s_g[c], s_b[c]);
+                }
+                const h4 q4 = cvt_h4(t);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hn[j + i] = q4[i];
+            }
+#pragma unroll
+            for (int rt = 0; rt < NPT; ++rt) acc[rt] = mfma_16x16x32(s_wr[(rt * KS + ks) * 64 + lane], hn, acc[rt]);
+        }
         float best_v = -3.0e38f;
         int best_e = 0x7fffffff;
-        for (int rt = 0; rt < a.np / 16; ++rt) {
-            f4 acc = f4_zero();
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) acc = mfma_16x16x32(load_frag(a.wr, rt * KS + ks, lane), hn[ks], acc);
+        for (int rt = 0; rt < NPT; ++rt) {
+            const h4 lg = cvt_h4(acc[rt]); /* logits are fp16 values */
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int e = 16 * rt + 4 * g + i;
-                const float lv = (float)(f16)(acc[i] + a.br[e]);
-                if (lv > best_v) { best_v = lv; best_e = e; }
+                const float lv = (float)lg[i];
+                if (lv > best_v) { best_v = lv; best_e = 16 * rt + 4 * g + i; }
             }
         }
         /* combine the 4 lane groups: larger logit wins, ties go to the lower id */
@@ -117,9 +153,16 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) prism_router_d256(RouterArgs a) {
-    router_body<256>(a);
-}
-extern "C" __global__ void __launch_bounds__(256) prism_router_d128(RouterArgs a) {
-    router_body<128>(a);
-}
+#define PRISM_ROUTER_KERNEL(D, NPT)                                                                 \
+    extern "C" __global__ void __launch_bounds__(256, 3) prism_router_d##D##_n##NPT(RouterArgs a) {\
+        router_body<D, NPT>(a);                                                                     \
+    }
+PRISM_ROUTER_KERNEL(256, 1)
+PRISM_ROUTER_KERNEL(256, 2)
+PRISM_ROUTER_KERNEL(256, 3)
+PRISM_ROUTER_KERNEL(256, 4)
+PRISM_ROUTER_KERNEL(128, 1)
+PRISM_ROUTER_KERNEL(128, 2)
+PRISM_ROUTER_KERNEL(128, 3)
+PRISM_ROUTER_KERNEL(128, 4)
+#undef PRISM_ROUTER_KERNEL
