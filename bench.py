@@ -149,24 +149,13 @@ def main():
     aux = hip.malloc(aux_n * 4)
     hip.memset(aux, 0, aux_n * 4)
     a_push = eng.attn_push(0, 0, n * d)
-    r_push = eng.router_push(0, T, n * d, 0, n, n + N + 1)
-    e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N + 1)
+    r_push = eng.router_push(0, T, n * d, 0, n, n + N)
+    e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N)
     log("[bench] per-stage timing")
     t_attn = time_stage(hip, lambda: eng.attn(a_push, feats, B, stream), args.stage_reps, stream)
-    # router and experts alternate so the counts are consumed between router launches
-    hip.sync()
-    rr = []
-    ee = []
-    for _ in range(args.stage_reps):
-        e0, e1, e2 = hip.event(), hip.event(), hip.event()
-        hip.record(e0, stream)
-        assert eng.router(r_push, feats, aux, B, stream) == 0
-        hip.record(e1, stream)
-        assert eng.experts(e_push, feats, aux, B, stream) == 0
-        hip.record(e2, stream)
-        rr.append(hip.elapsed_ms(e0, e1))
-        ee.append(hip.elapsed_ms(e1, e2))
-    t_router, t_expert = statistics.median(rr), statistics.median(ee)
+    # the router launch clears its counts itself; the expert stage only reads them
+    t_router = time_stage(hip, lambda: eng.router(r_push, feats, aux, B, stream), args.stage_reps, stream)
+    t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, aux, B, stream), args.stage_reps, stream)
     attn_flops = attn_flops_per_token(cfg) * n
     attn_tflops = attn_flops / (t_attn * 1e-3) / 1e12
 

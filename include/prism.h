@@ -85,10 +85,10 @@ typedef struct prism_attn_push {
  * {n_tokens, dim, n_experts, router_w, router_b, input_offset,
  *  assignment_offset, count_offset} + LN2 offsets + perm_offset.
  * aux layout: assignment [batch*n_tokens] int32 (expert id per token),
- * counts [n_experts + 1] (tokens per expert, then a completion ticket), and
- * perm [n_experts][batch*n_tokens] (token indices bucketed by expert: the
- * counting sort's output). counts must be zero on entry; the expert stage
- * returns them to zero when it has consumed them. */
+ * counts [n_experts] (tokens per expert), and perm [n_experts][batch*n_tokens]
+ * (token indices bucketed by expert: the counting sort's output; the order
+ * inside a bucket is unspecified). The launch clears counts itself (a fill
+ * kernel, then the router kernel), so nothing is required of them on entry. */
 typedef struct prism_router_push {
     int32_t n_tokens, dim, n_experts;
     int64_t router_w, router_b;
@@ -102,9 +102,9 @@ typedef struct prism_router_push {
  * {n_tokens, dim, expert_id, w1, b1, w2, b2, input_offset, output_offset,
  *  assignment_offset}, widened to ONE launch for all experts: expert_id is
  * replaced by n_experts + expert_stride (expert e at w1 + e*expert_stride),
- * and the router's count/perm regions are read instead of re-scanning the
- * assignment. n_experts == 1 with count_offset < 0 is the dense FFN stage
- * (every token, expert 0). */
+ * and the router's count/perm regions are read (not modified) instead of
+ * re-scanning the assignment. n_experts == 1 with count_offset < 0 is the
+ * dense FFN stage (every token, expert 0). */
 typedef struct prism_expert_push {
     int32_t n_tokens, dim, n_experts;
     int64_t w1, b1, w2, b2, expert_stride;
@@ -202,7 +202,7 @@ int prism_forward_assignments(prism_ctx* ctx, const int32_t** assign_dev,
 
 /* aux arena size in int32 elements that a router + expert pair needs for
  * n_experts experts and batch*n_tokens tokens when laid out as
- * [assignment | counts+ticket | perm]. */
+ * [assignment | counts | perm]. */
 int64_t prism_aux_elems(int32_t n_experts, int64_t tokens);
 
 #ifdef __cplusplus

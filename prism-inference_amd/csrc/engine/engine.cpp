@@ -13,6 +13,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -53,6 +54,7 @@ struct prism_ctx {
     hipFunction_t f_attn[2] = {};       /* [0] d128, [1] d256 */
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2] = {};     /* [dim], 64-token tiles */
+    hipFunction_t f_zero = nullptr;
     std::string err;
 
     bool loaded = false;
@@ -66,7 +68,7 @@ struct prism_ctx {
     uint16_t* ws_attn = nullptr;
     uint16_t* ws_scratch = nullptr;
     int32_t* ws_assign = nullptr; /* [n_blocks][n] */
-    int32_t* ws_counts = nullptr; /* [N + 1] */
+    int32_t* ws_counts = nullptr; /* [N] */
     int32_t* ws_perm = nullptr;   /* [N][n] */
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
@@ -144,6 +146,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_router[1][0], "prism_router_d256_n1"}, {&c->f_router[1][1], "prism_router_d256_n2"},
         {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
         {&c->f_expert[0], "prism_expert_d128_bm64"},  {&c->f_expert[1], "prism_expert_d256_bm64"},
+        {&c->f_zero, "prism_zero_i32"},
     };
     for (auto& f : fns) {
         e = hipModuleGetFunction(f.f, c->module, f.name);
@@ -360,7 +363,7 @@ int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s)
 }
 
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
-                 hipStream_t s) {
+                 hipStream_t s, int32_t* zero_counts = nullptr, int zero_n = 0) {
     const int D = c->desc.dim;
     AttnArgs a{};
     a.in = in;
@@ -376,9 +379,19 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     a.W = W;
     a.wx = (W + 7) / 8;
     a.windows_per_frame = a.wx * ((H + 7) / 8);
+    a.zero_counts = zero_counts;
+    a.zero_n = zero_n;
     const int64_t grid = (int64_t)a.windows_per_frame * batch;
     if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "attention grid %lld out of range", (long long)grid);
     return launch(c, c->f_attn[dim_index(D)], (unsigned)grid, a, s);
+}
+
+int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {
+    void* params[] = {&p, &n};
+    const unsigned grid = (unsigned)std::max(1, std::min(64, (n + 255) / 256));
+    hipError_t e = hipModuleLaunchKernel(c->f_zero, grid, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(zero): %s", hipGetErrorString(e));
+    return PRISM_OK;
 }
 
 int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t* assign, int32_t* counts,
@@ -397,11 +410,13 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
     a.n_experts = N;
     a.np = round16(N);
     a.cap = (int32_t)n;
-    const int64_t grid = (n + 127) / 128;
+    /* 2 tiles per wave at frame scale, up to 8 at large batch (fewer global atomics) */
+    a.tiles_per_wave = (int32_t)std::min<int64_t>(8, std::max<int64_t>(2, (n + 16383) / 16384));
+    const int64_t grid = (n + 64 * a.tiles_per_wave - 1) / (64 * a.tiles_per_wave);
     return launch(c, c->f_router[dim_index(c->desc.dim)][a.np / 16 - 1], (unsigned)grid, a, s);
 }
 
-int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int32_t* counts,
+int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, const int32_t* counts,
                     const int32_t* perm, int64_t n, hipStream_t s) {
     const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
     ExpertArgs a{};
@@ -482,6 +497,8 @@ extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void
     const uint16_t* f = static_cast<const uint16_t*>(features);
     if (!aligned16(f + p->input_offset)) return fail(c, PRISM_ERR_INVALID, "input_offset must be a multiple of 8");
     HIP_TRY(c, hipSetDevice(c->device));
+    const int rc = enqueue_zero(c, aux + p->count_offset, p->n_experts, (hipStream_t)stream);
+    if (rc) return rc;
     return enqueue_router(c, *k, f + p->input_offset, aux + p->assignment_offset, aux + p->count_offset,
                           aux + p->perm_offset, n, (hipStream_t)stream);
 }
@@ -527,7 +544,7 @@ static int ensure_workspace(prism_ctx* c, int batch) {
     const size_t o_attn = ar.take((size_t)n * D * 2);
     const size_t o_scr = ar.take((size_t)n * D * 2);
     const size_t o_asg = ar.take((size_t)NB * n * 4);
-    const size_t o_cnt = ar.take((size_t)(N + 1) * 4);
+    const size_t o_cnt = ar.take((size_t)N * 4);
     const size_t o_perm = ar.take((size_t)N * n * 4);
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, ar.off);
@@ -561,7 +578,9 @@ static int enqueue_forward(prism_ctx* c, const uint16_t* in, uint16_t* out, int 
     for (int b = 0; b < NB; ++b) {
         const DevBlock& k = c->blocks[b];
         uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : c->ws_scratch;
-        int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s);
+        /* the attention kernel clears the counts its router accumulates into */
+        int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s, moe ? c->ws_counts : nullptr,
+                              moe ? c->desc.n_experts : 0);
         if (rc) return rc;
         if (moe) {
             rc = enqueue_router(c, k, c->ws_attn, c->ws_assign + (size_t)b * n, c->ws_counts, c->ws_perm, n, s);

@@ -235,7 +235,7 @@ extern "C" int prism_pack_weight(const uint16_t* w, int32_t rows, int32_t k, int
 
 extern "C" int64_t prism_aux_elems(int32_t n_experts, int64_t tokens) {
     if (n_experts < 1 || tokens < 0) return -1;
-    return tokens + (n_experts + 1) + (int64_t)n_experts * tokens;
+    return tokens + n_experts + (int64_t)n_experts * tokens;
 }
 
 extern "C" int prism_histogram(const int32_t* assign, int64_t n, int32_t n_experts, int64_t* counts) {

@@ -29,6 +29,9 @@ typedef struct AttnArgs {
     int32_t H, W;         /* token grid                                  */
     int32_t wx;           /* windows per row = ceil(W/8)                 */
     int32_t windows_per_frame;
+    int32_t* zero_counts; /* if set, workgroup 0 zeroes zero_n ints here  */
+    int32_t zero_n;       /* (the next router's counts, block chain only) */
+    int32_t pad_;
 } AttnArgs;
 
 typedef struct RouterArgs {
@@ -38,12 +41,14 @@ typedef struct RouterArgs {
     const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts are 0 */
     const float* br;      /* [np]; entries >= n_experts are -inf          */
     int32_t* assign;      /* [n_tokens] expert id                         */
-    int32_t* counts;      /* [n_experts + 1]: per-expert totals, ticket   */
+    int32_t* counts;      /* [n_experts] per-expert totals (zero on entry) */
     int32_t* perm;        /* [n_experts][cap] token ids bucketed by expert */
     int32_t n_tokens;     /* tokens in this launch (batch * per-frame)     */
     int32_t n_experts;
     int32_t np;           /* n_experts rounded up to 16                    */
     int32_t cap;          /* bucket capacity = n_tokens                    */
+    int32_t tiles_per_wave; /* 16-token tiles per wave: WG = 64*tiles tokens */
+    int32_t pad_;
 } RouterArgs;
 
 typedef struct ExpertArgs {
@@ -55,7 +60,7 @@ typedef struct ExpertArgs {
     const float* b1;      /* [n_experts][dim]                             */
     const uint16_t* w2;
     const float* b2;
-    int32_t* counts;      /* NULL = dense stage (every token, expert 0)   */
+    const int32_t* counts; /* [n_experts]; NULL = dense stage (expert 0)  */
     const int32_t* perm;  /* [n_experts][cap]                             */
     int32_t n_tokens;
     int32_t n_experts;

@@ -99,6 +99,11 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p, loff);
     sched_fence();
 
+    /* block chain only: clear the counts the following router accumulates into
+     * (the previous expert stage, which read them, finished before this launch) */
+    if (a.zero_counts && blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.zero_n; i += 256) a.zero_counts[i] = 0;
+
     for (int i = threadIdx.x; i < 3 * DIM; i += 256) s_bqkv[i] = a.bqkv[i];
     for (int i = threadIdx.x; i < DIM; i += 256) {
         s_bo[i] = a.bo[i];

@@ -23,9 +23,6 @@
  * (in flight during GEMM1 and the GELU); GEMM2 issues the second half of W2
  * while it consumes the first.
  *
- * Counts ticket: every workgroup, active or not, takes a ticket at the end;
- * the last one returns counts[0..N] to zero for the next router launch.
- *
  * GEMMs are C^T = W * A^T (weights as the A operand, tokens as columns), so a
  * lane's accumulator holds 4 consecutive channels of one token: 8-byte LDS
  * writes for the GELU tile and 8-byte global stores for the output rows,
@@ -208,19 +205,6 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         }
     }
 
-    /* ---- counts ticket --------------------------------------------------- */
-    if (a.counts) {
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            const int prev = atomicAdd(&a.counts[a.n_experts], 1);
-            if (prev == (int)gridDim.x - 1) {
-                for (int i = 0; i < a.n_experts; ++i) atomicExch(&a.counts[i], 0);
-                atomicExch(&a.counts[a.n_experts], 0);
-                __threadfence();
-            }
-        }
-    }
 }
 
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm64(ExpertArgs a) {

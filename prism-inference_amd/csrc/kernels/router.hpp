@@ -10,9 +10,14 @@
  * rank then places it in its expert's bucket of `perm`, which is the
  * expert-contiguous segment the grouped expert GEMM consumes.
  *
- * Workgroup = 4 waves x 32 tokens. A lane owns one token of a 16-token tile
- * and the 8-channel slices 32*ks + 8*g .. +7 of it, which is exactly the
- * B-operand fragment of logits^T = W_r * hn^T, so LN2 runs in registers.
+ * Workgroup = 4 waves, each taking `tiles_per_wave` consecutive 16-token
+ * tiles (2 at small batch, up to 8 at large batch, so a big launch issues
+ * 4x fewer global atomics); the next tile's rows are loaded while the current
+ * one is computed. A lane owns one token of a tile and the 8-channel slices
+ * 32*ks + 8*g .. +7 of it, which is exactly the B-operand fragment of
+ * logits^T = W_r * hn^T, so LN2 runs in registers. Each token's expert and
+ * LDS rank are parked in LDS and scattered after the workgroup's bucket bases
+ * are known.
  * NPT = padded experts / 16 is a template parameter; the workgroup copies
  * the NPT*KS router fragments into LDS once and every wave reads them from
  * there, which keeps the register count low enough for several workgroups
@@ -21,34 +26,38 @@
 #pragma once
 #include "common.hpp"
 
-#define ROUTER_TOKENS_PER_WG 128
+#define ROUTER_MAX_TILES_PER_WAVE 8
+
+template <int DIM, int KS>
+__device__ __forceinline__ void router_load_tile(const RouterArgs& a, int token, int g, h8 (&xr)[KS]) {
+    const uint16_t* row = a.in + (int64_t)(token < a.n_tokens ? token : 0) * DIM;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        xr[ks] = token < a.n_tokens ? *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g) : h8{};
+}
 
 template <int DIM, int NPT>
 __device__ __forceinline__ void router_body(const RouterArgs& a) {
     constexpr int KS = DIM / 32;
-    constexpr int TT = 2;            /* token tiles per wave */
-    constexpr int NF = NPT * KS;     /* router fragments     */
+    constexpr int NF = NPT * KS;     /* router fragments */
+    constexpr int MAXTOK = 4 * ROUTER_MAX_TILES_PER_WAVE * 16;
     __shared__ int hist[64];
     __shared__ int base[64];
     __shared__ float s_g[DIM], s_b[DIM], s_br[16 * NPT];
     __shared__ __attribute__((aligned(16))) h8 s_wr[NF * 64]; /* fragment-ordered W_r */
+    __shared__ int s_e[MAXTOK], s_rank[MAXTOK];
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
+    const int tpw = a.tiles_per_wave;
+    const int wg_tokens = 64 * tpw;
+    const int tok_wg0 = blockIdx.x * wg_tokens;
 
-    /* this wave's token rows first, then the cooperative W_r copy */
-    const int tok0 = blockIdx.x * ROUTER_TOKENS_PER_WG + wave * 16 * TT;
-    h8 xr[TT][KS];
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        const int token = tok0 + 16 * tt + l16;
-        const uint16_t* row = a.in + (int64_t)(token < a.n_tokens ? token : 0) * DIM;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            xr[tt][ks] = token < a.n_tokens ? *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g) : h8{};
-    }
+    /* first tile's rows, then the cooperative W_r copy and parameters */
+    h8 xr[KS];
+    router_load_tile<DIM, KS>(a, tok_wg0 + wave * tpw * 16 + l16, g, xr);
     {
         const FragSrc src_r(a.wr, 16u * NPT * DIM * 2u);
         for (int i = threadIdx.x; i < NF * 64; i += 256) s_wr[i] = src_r.load(i / 64, (i % 64) * 16);
@@ -61,17 +70,21 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
     for (int i = threadIdx.x; i < 16 * NPT; i += 256) s_br[i] = a.br[i];
     __syncthreads();
 
-    int my_e[TT], my_rank[TT];
+#pragma unroll 1
+    for (int it = 0; it < tpw; ++it) {
+        const int local = (wave * tpw + it) * 16 + l16;
+        const int token = tok_wg0 + local;
+        h8 cur[KS];
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        const int token = tok0 + 16 * tt + l16;
-        const bool valid = token < a.n_tokens;
+        for (int ks = 0; ks < KS; ++ks) cur[ks] = xr[ks];
+        if (it + 1 < tpw) router_load_tile<DIM, KS>(a, token + 16, g, xr); /* next tile in flight */
+
         /* LN2 in registers: this lane holds channels 32ks + 8g + j */
         float s = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s += (float)xr[tt][ks][j];
+            for (int j = 0; j < 8; ++j) s += (float)cur[ks][j];
         s += __shfl_xor(s, 16, 64);
         s += __shfl_xor(s, 32, 64);
         const float mean = s * (1.0f / DIM);
@@ -80,7 +93,7 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float t = (float)xr[tt][ks][j] - mean;
+                const float t = (float)cur[ks][j] - mean;
                 q = __builtin_fmaf(t, t, q);
             }
         q += __shfl_xor(q, 16, 64);
@@ -103,7 +116,7 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int c = 32 * ks + 8 * g + j + i;
-                    t[i] = __builtin_fmaf((float)xr[tt][ks][j + i] - mean, inv * s_g[c], s_b[c]);
+                    t[i] = __builtin_fmaf((float)cur[ks][j + i] - mean, inv * s_g[c], s_b[c]);
                 }
                 const h4 q4 = cvt_h4(t);
 #pragma unroll
@@ -131,9 +144,10 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
             if (ov > best_v || (ov == best_v && oe < best_e)) { best_v = ov; best_e = oe; }
         }
         if (best_e >= a.n_experts || best_e < 0) best_e = 0; /* non-finite logits */
-        my_e[tt] = best_e;
-        my_rank[tt] = 0;
-        if (valid && g == 0) my_rank[tt] = atomicAdd(&hist[best_e], 1);
+        if (g == 0) {
+            s_e[local] = best_e;
+            s_rank[local] = token < a.n_tokens ? atomicAdd(&hist[best_e], 1) : 0;
+        }
     }
     __syncthreads();
     if (threadIdx.x < a.n_experts) {
@@ -141,13 +155,12 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
         base[threadIdx.x] = c ? atomicAdd(&a.counts[threadIdx.x], c) : 0;
     }
     __syncthreads();
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        const int token = tok0 + 16 * tt + l16;
-        if (token < a.n_tokens && g == 0) {
-            const int e = my_e[tt];
+    for (int j = threadIdx.x; j < wg_tokens; j += 256) {
+        const int token = tok_wg0 + j;
+        if (token < a.n_tokens) {
+            const int e = s_e[j];
             a.assign[token] = e;
-            const int slot = base[e] + my_rank[tt];
+            const int slot = base[e] + s_rank[j];
             if (slot < a.cap) a.perm[(int64_t)e * a.cap + slot] = token;
         }
     }

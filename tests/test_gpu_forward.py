@@ -77,7 +77,7 @@ def test_blocks_teacher_forced(hip, engine, device_arena, name, nb, H, W, batch)
     feats = device_arena(3 * n * d * 2)
     aux_n = P.aux_elems(N, n)
     aux = device_arena(aux_n * 4)
-    a_off, c_off, p_off = 0, n, n + N + 1
+    a_off, c_off, p_off = 0, n, n + N
     cur = x
     for b in range(nb):
         print(f"[blocks] {name} block {b}", flush=True)
