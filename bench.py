@@ -68,6 +68,21 @@ def time_stage(hip, launch, reps, stream):
     return hip.elapsed_ms(e0, e1) / reps
 
 
+def measured_traffic(kernel, grid):
+    """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (calibrated against a device copy of known size), if it covers this
+    kernel at this grid; None otherwise."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_moe64_b16.txt")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("bench_traffic "):
+            kv = dict(item.split("=", 1) for item in line.split()[1:])
+            if kv.get("kernel") == kernel and int(kv.get("grid", -1)) == grid:
+                return int(kv["traffic_bytes"]), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def cpu_baseline(cfg, blob, offs, x_bits, budget_s):
     """The oracle (fp32 C + OpenMP) on the host cores, one frame at a time."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -158,6 +173,8 @@ def main():
     t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, aux, B, stream), args.stage_reps, stream)
     attn_flops = attn_flops_per_token(cfg) * n
     attn_tflops = attn_flops / (t_attn * 1e-3) / 1e12
+    attn_grid = ((cfg.W + 7) // 8) * ((cfg.H + 7) // 8) * B
+    traffic, traffic_src = measured_traffic("prism_attn_d256", attn_grid) if cfg.name == "moe64" else (None, None)
 
     # ---- expert load actually produced (all blocks, batch B)
     share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
@@ -189,7 +206,9 @@ def main():
                       "batch": B},
         "roofline": {"kernel": "prism_attn_d256", "bound": "mfma", "achieved": round(attn_tflops, 2),
                      "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": None,
+                     "frac": round(attn_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "traffic_source": traffic_src,
                      "flops_per_launch": attn_flops, "avg_launch_ms": round(t_attn, 5)},
         "expert_load": {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
                         "hottest_share_mean": round(float(share.mean()), 4),
