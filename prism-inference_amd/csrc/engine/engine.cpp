@@ -51,7 +51,7 @@ using namespace prism;
 struct prism_ctx {
     int device = 0;
     hipModule_t module = nullptr;
-    hipFunction_t f_attn[2] = {};       /* [0] d128, [1] d256 */
+    hipFunction_t f_attn[2][2] = {};    /* [d128, d256][4 waves, 8 waves] */
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2] = {};     /* [dim], 64-token tiles */
     hipFunction_t f_zero = nullptr;
@@ -140,7 +140,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         return fail(nullptr, PRISM_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
     }
     struct { hipFunction_t* f; const char* name; } fns[] = {
-        {&c->f_attn[0], "prism_attn_d128"},         {&c->f_attn[1], "prism_attn_d256"},
+        {&c->f_attn[0][0], "prism_attn_d128"},      {&c->f_attn[1][0], "prism_attn_d256"},
+        {&c->f_attn[0][1], "prism_attn_d128_w8"},   {&c->f_attn[1][1], "prism_attn_d256_w8"},
         {&c->f_router[0][0], "prism_router_d128_n1"}, {&c->f_router[0][1], "prism_router_d128_n2"},
         {&c->f_router[0][2], "prism_router_d128_n3"}, {&c->f_router[0][3], "prism_router_d128_n4"},
         {&c->f_router[1][0], "prism_router_d256_n1"}, {&c->f_router[1][1], "prism_router_d256_n2"},
@@ -355,9 +356,9 @@ extern "C" int prism_load_weights_file(prism_ctx* c, const prism_model_desc* d, 
 namespace {
 
 template <class A>
-int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s) {
+int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s, unsigned block = 256) {
     void* params[] = {&args};
-    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
     return PRISM_OK;
 }
@@ -383,7 +384,10 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     a.zero_n = zero_n;
     const int64_t grid = (int64_t)a.windows_per_frame * batch;
     if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "attention grid %lld out of range", (long long)grid);
-    return launch(c, c->f_attn[dim_index(D)], (unsigned)grid, a, s);
+    /* fewer than two windows per CU: one 8-wave workgroup per window (a head per
+     * wave) shortens each window's serial path; otherwise 4 waves x 2 per CU */
+    const int w8 = grid < 512 ? 1 : 0;
+    return launch(c, c->f_attn[dim_index(D)][w8], (unsigned)grid, a, s, w8 ? 512u : 256u);
 }
 
 int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {

@@ -6,7 +6,7 @@
  * out-proj + fp16 residual :71-78) with the pre-LayerNorm added, as:
  *
  *  1. LN1 of the window's 64 slots -> xs (LDS, fp16). Padded slots are zero.
- *  2. Wave w owns heads w and w+4. Per head, one MFMA GEMM pass over the
+ *  2. Wave w owns heads w and w+4 (8-wave variant: head w). Per head, one MFMA GEMM pass over the
  *     model dim produces Q^T and K^T (rows = channel, cols = token) and V
  *     (rows = token, cols = channel), fp32 accumulate, bias, fp16 round.
  *  3. S^T = K Q^T is one MFMA per 16x16 tile straight from those registers:
@@ -28,15 +28,16 @@
 #pragma once
 #include "common.hpp"
 
-template <int DIM, int HD>
+template <int DIM, int HD, int NW>
 struct AttnShape {
     static constexpr int KS = DIM / 32;            /* k-steps over the model dim     */
     static constexpr int CT = HD / 16;             /* 16-channel tiles per head      */
     static constexpr int FPK = 3 * CT;             /* QKV fragments per k-step       */
     static constexpr int HEADF = KS * FPK;         /* fragments per head             */
-    static constexpr int ORT = DIM / 64;           /* out-proj row tiles per wave    */
+    static constexpr int HPW = 8 / NW;             /* heads per wave                 */
+    static constexpr int ORT = DIM / 16 / NW;      /* out-proj row tiles per wave    */
     static constexpr int OUTF = KS * ORT;          /* out-proj fragments             */
-    static constexpr int TOTAL = 2 * HEADF + OUTF; /* fragment sequence length       */
+    static constexpr int TOTAL = HPW * HEADF + OUTF; /* fragment sequence length     */
     static constexpr int PF = 2 * FPK;             /* ring depth (2 k-steps ahead)   */
     static constexpr int LDS = DIM + 8;            /* padded LDS row, halfs          */
 };
@@ -44,26 +45,28 @@ struct AttnShape {
 /* Fragment p of wave `wave`'s sequence: head A's QKV k-steps, head B's, then
  * the out-proj's (p is a compile-time constant or depends only on the head
  * index, so both branches are wave-uniform). */
-template <int DIM, int HD>
+template <int DIM, int HD, int NW>
 __device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, int wave, int p, int loff) {
-    using S = AttnShape<DIM, HD>;
-    if (p < 2 * S::HEADF) {
+    using S = AttnShape<DIM, HD, NW>;
+    if (p < S::HPW * S::HEADF) {
         const int hh = p / S::HEADF, q = p % S::HEADF;
         const int ks = q / S::FPK, f = q % S::FPK;
         const int mat = f / S::CT, c = f % S::CT; /* 0 = Q, 1 = K, 2 = V */
-        const int h = wave + 4 * hh;
+        const int h = wave + NW * hh;
         const int rt = (mat * DIM + h * HD) / 16 + c;
         return wqkv.load(rt * S::KS + ks, loff);
     }
-    const int q = p - 2 * S::HEADF;
+    const int q = p - S::HPW * S::HEADF;
     const int ks = q / S::ORT, r = q % S::ORT;
     return wo.load((wave * S::ORT + r) * S::KS + ks, loff);
 }
 
-template <int DIM, int HD>
+template <int DIM, int HD, int NW>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     static_assert(DIM / HD == 8, "8 heads");
-    using S = AttnShape<DIM, HD>;
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    using S = AttnShape<DIM, HD, NW>;
+    constexpr int NT = 64 * NW;         /* threads                         */
     constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT, PF = S::PF;
     constexpr float LOG2E = 1.4426950408889634f;
     const float scale = (HD == 32) ? 0.1767766953f : 1.0f / sqrtf((float)HD);
@@ -96,16 +99,16 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     /* weight ring: first PF fragments go out before anything else */
     h8 ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p, loff);
+    for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p, loff);
     sched_fence();
 
     /* block chain only: clear the counts the following router accumulates into
      * (the previous expert stage, which read them, finished before this launch) */
     if (a.zero_counts && blockIdx.x == 0)
-        for (int i = threadIdx.x; i < a.zero_n; i += 256) a.zero_counts[i] = 0;
+        for (int i = threadIdx.x; i < a.zero_n; i += NT) a.zero_counts[i] = 0;
 
-    for (int i = threadIdx.x; i < 3 * DIM; i += 256) s_bqkv[i] = a.bqkv[i];
-    for (int i = threadIdx.x; i < DIM; i += 256) {
+    for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
+    for (int i = threadIdx.x; i < DIM; i += NT) {
         s_bo[i] = a.bo[i];
         s_g[i] = a.ln_g[i];
         s_b[i] = a.ln_b[i];
@@ -114,13 +117,14 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     /* ---- 1. LN1: all row loads first, then the math ------------------ */
     {
         constexpr int LPS = DIM / 16;
-        constexpr int SPI = 64 / LPS; /* slots per wave iteration */
-        constexpr int IT = 16 / SPI;
+        constexpr int SPI = 64 / LPS;   /* slots per wave iteration */
+        constexpr int SPW = 64 / NW;    /* slots per wave           */
+        constexpr int IT = SPW / SPI;
         RowChunk rc[IT];
         bool valid[IT];
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
-            const int s = wave * 16 + it * SPI + lane / LPS;
+            const int s = wave * SPW + it * SPI + lane / LPS;
             const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
             valid[it] = gy < a.H && gx < a.W;
             rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
@@ -128,18 +132,18 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
         __syncthreads(); /* LN parameters staged */
 #pragma unroll
         for (int it = 0; it < IT; ++it)
-            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * 16 + it * SPI + lane / LPS) * LDS, nullptr);
+            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * SPW + it * SPI + lane / LPS) * LDS, nullptr);
     }
     __syncthreads();
 
     /* ---- 2./3. per head ----------------------------------------------- */
     static_assert(S::HEADF % PF == 0, "ring slots must not depend on the head index");
 #pragma unroll 1
-    for (int hh = 0; hh < 2; ++hh) {
+    for (int hh = 0; hh < S::HPW; ++hh) {
         /* keeps the head-invariant xs reads inside the loop (hoisting all of
          * them out would pin 32 fragments in registers) */
         asm volatile("" ::: "memory");
-        const int h = wave + 4 * hh;
+        const int h = wave + NW * hh;
         /* accumulators start at the bias, so the MFMAs add it.
          * Q^T/K^T element i: channel 16c+4g+i, token 16t+l16.
          * V element i: token 16t+4g+i, channel 16c+l16. */
@@ -171,7 +175,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                     else if (mat == 1) accK[c][t] = mfma_16x16x32(w, xf[t], accK[c][t]);
                     else accV[t][c] = mfma_16x16x32(xf[t], w, accV[t][c]);
                 }
-                ring[p % PF] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p + PF, loff); /* p + PF < TOTAL here */
+                if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p + PF, loff);
             }
             sched_fence();
         }
@@ -286,11 +290,11 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             of[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
-            const int p = 2 * S::HEADF + ks * ORT + r;
+            const int p = S::HPW * S::HEADF + ks * ORT + r;
             const h8 w = ring[p % PF];
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
-            if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD>(src_qkv, src_o, wave, p + PF, loff);
+            if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p + PF, loff);
         }
         sched_fence();
     }
@@ -307,9 +311,17 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     }
 }
 
+/* 4 waves (2 heads each, 2 workgroups per CU) for large grids; 8 waves (one
+ * head each, one workgroup per CU) when windows are scarcer than CUs. */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d256(AttnArgs a) {
-    attn_window_body<256, 32>(a);
+    attn_window_body<256, 32, 4>(a);
 }
 extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128(AttnArgs a) {
-    attn_window_body<128, 16>(a);
+    attn_window_body<128, 16, 4>(a);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d256_w8(AttnArgs a) {
+    attn_window_body<256, 32, 8>(a);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d128_w8(AttnArgs a) {
+    attn_window_body<128, 16, 8>(a);
 }

@@ -42,6 +42,8 @@ def tok_ids(n):
     ("moe64", 12, 20, 3),       # ragged windows on both axes, 3 frames
     ("moe32", 135, 240, 1),     # 1080p-native grid, 510 windows
     ("std256", 8, 8, 2),        # exactly one window per frame
+    ("moe64", 68, 120, 4),      # 540 windows: the 4-wave kernel
+    ("dense128", 68, 120, 4),   # 4-wave kernel, 8 heads x 16
 ])
 def test_attention_stage(hip, engine, device_arena, name, H, W, batch):
     cfg = P.CONFIGS[name]
