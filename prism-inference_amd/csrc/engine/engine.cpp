@@ -48,12 +48,17 @@ struct DevBlock {
 
 using namespace prism;
 
+/* The chain's per-expert counters sit 256 bytes apart: every workgroup of a
+ * routed attention launch adds to them, and counters sharing a cache line
+ * would serialise those atomics in one memory channel. */
+static constexpr int CHAIN_COUNT_STRIDE = 64;
+
 struct prism_ctx {
     int device = 0;
     hipModule_t module = nullptr;
-    hipFunction_t f_attn[2][2] = {};    /* [d128, d256][4 waves, 8 waves] */
+    hipFunction_t f_attn[2][2][5] = {}; /* [d128, d256][4 waves, 8 waves][routed: padded experts / 16] */
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
-    hipFunction_t f_expert[2] = {};     /* [dim], 64-token tiles */
+    hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
     hipFunction_t f_zero = nullptr;
     std::string err;
 
@@ -68,10 +73,11 @@ struct prism_ctx {
     uint16_t* ws_attn = nullptr;
     uint16_t* ws_scratch = nullptr;
     int32_t* ws_assign = nullptr; /* [n_blocks][n] */
-    int32_t* ws_counts = nullptr; /* [N] */
+    int32_t* ws_counts = nullptr; /* [n_blocks][N][CHAIN_COUNT_STRIDE] */
     int32_t* ws_perm = nullptr;   /* [N][n] */
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
+    bool counts_dirty = false;    /* block 0's counters may be nonzero */
 
     hipStream_t cap_stream = nullptr;
     hipGraph_t graph = nullptr;
@@ -140,21 +146,27 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         return fail(nullptr, PRISM_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
     }
     struct { hipFunction_t* f; const char* name; } fns[] = {
-        {&c->f_attn[0][0], "prism_attn_d128"},      {&c->f_attn[1][0], "prism_attn_d256"},
-        {&c->f_attn[0][1], "prism_attn_d128_w8"},   {&c->f_attn[1][1], "prism_attn_d256_w8"},
         {&c->f_router[0][0], "prism_router_d128_n1"}, {&c->f_router[0][1], "prism_router_d128_n2"},
         {&c->f_router[0][2], "prism_router_d128_n3"}, {&c->f_router[0][3], "prism_router_d128_n4"},
         {&c->f_router[1][0], "prism_router_d256_n1"}, {&c->f_router[1][1], "prism_router_d256_n2"},
         {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
-        {&c->f_expert[0], "prism_expert_d128_bm64"},  {&c->f_expert[1], "prism_expert_d256_bm64"},
+        {&c->f_expert[0][0], "prism_expert_d128_bm64"},  {&c->f_expert[1][0], "prism_expert_d256_bm64"},
+        {&c->f_expert[0][1], "prism_expert_d128_bm64_w8"}, {&c->f_expert[1][1], "prism_expert_d256_bm64_w8"},
         {&c->f_zero, "prism_zero_i32"},
     };
-    for (auto& f : fns) {
-        e = hipModuleGetFunction(f.f, c->module, f.name);
+    std::vector<std::pair<hipFunction_t*, std::string>> all;
+    for (auto& f : fns) all.emplace_back(f.f, f.name);
+    for (int di = 0; di < 2; ++di)
+        for (int w8 = 0; w8 < 2; ++w8)
+            for (int r = 0; r <= 4; ++r)
+                all.emplace_back(&c->f_attn[di][w8][r], std::string("prism_attn_d") + (di ? "256" : "128") +
+                                                            (w8 ? "_w8" : "") + (r ? "_r" + std::to_string(r) : ""));
+    for (auto& f : all) {
+        e = hipModuleGetFunction(f.first, c->module, f.second.c_str());
         if (e != hipSuccess) {
             (void)hipModuleUnload(c->module);
             delete c;
-            return fail(nullptr, PRISM_ERR_CODE_OBJECT, "kernel %s missing from %s: %s", f.name, path.c_str(),
+            return fail(nullptr, PRISM_ERR_CODE_OBJECT, "kernel %s missing from %s: %s", f.second.c_str(), path.c_str(),
                         hipGetErrorString(e));
         }
     }
@@ -363,8 +375,17 @@ int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s,
     return PRISM_OK;
 }
 
+/* Routing outputs of a routed attention launch (block chain, MoE blocks). */
+struct RouteOut {
+    int32_t* assign;
+    int32_t* counts; /* zero on entry; expert e at counts[e * count_stride] */
+    int32_t* perm;
+    int32_t count_stride;
+    int32_t* zero_next; /* counters this launch clears for a later one, or NULL */
+};
+
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
-                 hipStream_t s, int32_t* zero_counts = nullptr, int zero_n = 0) {
+                 hipStream_t s, const RouteOut* route = nullptr) {
     const int D = c->desc.dim;
     AttnArgs a{};
     a.in = in;
@@ -380,14 +401,28 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     a.W = W;
     a.wx = (W + 7) / 8;
     a.windows_per_frame = a.wx * ((H + 7) / 8);
-    a.zero_counts = zero_counts;
-    a.zero_n = zero_n;
+    int npt = 0;
+    if (route) {
+        const int N = c->desc.n_experts;
+        npt = round16(N) / 16;
+        a.ln2_g = k.ln2_g;
+        a.ln2_b = k.ln2_b;
+        a.wr = k.wr;
+        a.br = k.br;
+        a.assign = route->assign;
+        a.counts = route->counts;
+        a.perm = route->perm;
+        a.n_experts = N;
+        a.cap = (int32_t)((int64_t)batch * H * W);
+        a.count_stride = route->count_stride;
+        a.zero_next = route->zero_next;
+    }
     const int64_t grid = (int64_t)a.windows_per_frame * batch;
     if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "attention grid %lld out of range", (long long)grid);
     /* fewer than two windows per CU: one 8-wave workgroup per window (a head per
      * wave) shortens each window's serial path; otherwise 4 waves x 2 per CU */
     const int w8 = grid < 512 ? 1 : 0;
-    return launch(c, c->f_attn[dim_index(D)][w8], (unsigned)grid, a, s, w8 ? 512u : 256u);
+    return launch(c, c->f_attn[dim_index(D)][w8][npt], (unsigned)grid, a, s, w8 ? 512u : 256u);
 }
 
 int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {
@@ -421,7 +456,7 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
 }
 
 int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, const int32_t* counts,
-                    const int32_t* perm, int64_t n, hipStream_t s) {
+                    const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1) {
     const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
     ExpertArgs a{};
     a.in = in;
@@ -437,10 +472,13 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     a.n_tokens = (int32_t)n;
     a.n_experts = N;
     a.cap = (int32_t)n;
+    a.count_stride = count_stride;
     const int64_t bm = 64;
     int64_t tiles = (n + bm - 1) / bm + (counts ? N : 0);
     tiles = (tiles + 7) / 8 * 8;
-    return launch(c, c->f_expert[dim_index(D)], (unsigned)tiles, a, s);
+    /* fewer tiles than two per CU: 8 waves per tile halve each wave's weight stream */
+    const int w8 = tiles < 512 ? 1 : 0;
+    return launch(c, c->f_expert[dim_index(D)][w8], (unsigned)tiles, a, s, w8 ? 512u : 256u);
 }
 
 /* which: 0 = attention (qkv_w), 1 = router (router_w), 2 = experts (exp_w1) */
@@ -548,7 +586,7 @@ static int ensure_workspace(prism_ctx* c, int batch) {
     const size_t o_attn = ar.take((size_t)n * D * 2);
     const size_t o_scr = ar.take((size_t)n * D * 2);
     const size_t o_asg = ar.take((size_t)NB * n * 4);
-    const size_t o_cnt = ar.take((size_t)N * 4);
+    const size_t o_cnt = ar.take((size_t)NB * N * CHAIN_COUNT_STRIDE * 4);
     const size_t o_perm = ar.take((size_t)N * n * 4);
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, ar.off);
@@ -567,36 +605,59 @@ static int ensure_workspace(prism_ctx* c, int batch) {
     c->ws_assign = reinterpret_cast<int32_t*>(b + o_asg);
     c->ws_counts = reinterpret_cast<int32_t*>(b + o_cnt);
     c->ws_perm = reinterpret_cast<int32_t*>(b + o_perm);
+    c->counts_dirty = false; /* zero-filled above */
     return PRISM_OK;
 }
 
 /* Block b reads the previous block's output (block 0 reads `in`) and writes
  * `out` if (n_blocks-1-b) is even, the scratch buffer otherwise, so the last
- * block always lands in `out` and `in` is only read. */
-static int enqueue_forward(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
+ * block always lands in `out` and `in` is only read. MoE blocks run two
+ * launches: attention with fused routing, then the experts. Each block has
+ * its own row of counters; block b's attention launch clears block b+1's
+ * row, and the last block clears block 0's for the next chain, so a complete
+ * chain leaves row 0 at zero. The workspace starts zeroed; a one-block model
+ * clears its row inside the chain; after a chain that failed part-way, the
+ * next prism_forward / prism_forward_graph call clears row 0 first. */
+static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
     const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w;
     const int64_t n = (int64_t)batch * H * W;
     const bool moe = c->desc.n_experts > 1;
     c->fwd_tokens = n;
+    const int N = c->desc.n_experts;
+    const size_t row = (size_t)N * CHAIN_COUNT_STRIDE;
+    if (moe && NB == 1) {
+        const int rc = enqueue_zero(c, c->ws_counts, (int32_t)row, s);
+        if (rc) return rc;
+    }
     const uint16_t* src = in;
     for (int b = 0; b < NB; ++b) {
         const DevBlock& k = c->blocks[b];
         uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : c->ws_scratch;
-        /* the attention kernel clears the counts its router accumulates into */
-        int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s, moe ? c->ws_counts : nullptr,
-                              moe ? c->desc.n_experts : 0);
-        if (rc) return rc;
         if (moe) {
-            rc = enqueue_router(c, k, c->ws_attn, c->ws_assign + (size_t)b * n, c->ws_counts, c->ws_perm, n, s);
+            int32_t* counts = c->ws_counts + (size_t)b * row;
+            const RouteOut ro{c->ws_assign + (size_t)b * n, counts, c->ws_perm, CHAIN_COUNT_STRIDE,
+                              NB > 1 ? c->ws_counts + (size_t)((b + 1) % NB) * row : nullptr};
+            int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s, &ro);
             if (rc) return rc;
-            rc = enqueue_experts(c, k, c->ws_attn, dst, c->ws_counts, c->ws_perm, n, s);
+            rc = enqueue_experts(c, k, c->ws_attn, dst, counts, c->ws_perm, n, s, CHAIN_COUNT_STRIDE);
+            if (rc) return rc;
         } else {
+            int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s);
+            if (rc) return rc;
             rc = enqueue_experts(c, k, c->ws_attn, dst, nullptr, nullptr, n, s);
+            if (rc) return rc;
         }
-        if (rc) return rc;
         src = dst;
     }
     return PRISM_OK;
+}
+
+/* Clears block 0's counters on `s` if a failed chain may have left them set. */
+static int clean_counts(prism_ctx* c, hipStream_t s) {
+    if (!c->counts_dirty || c->desc.n_experts < 2) return PRISM_OK;
+    const int rc = enqueue_zero(c, c->ws_counts, c->desc.n_experts * CHAIN_COUNT_STRIDE, s);
+    if (rc == PRISM_OK) c->counts_dirty = false;
+    return rc;
 }
 
 static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
@@ -614,8 +675,12 @@ extern "C" int prism_forward(prism_ctx* c, const void* in, void* out, int32_t ba
     HIP_TRY(c, hipSetDevice(c->device));
     rc = ensure_workspace(c, batch);
     if (rc) return rc;
-    return enqueue_forward(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
-                           (hipStream_t)stream);
+    rc = clean_counts(c, (hipStream_t)stream);
+    if (rc) return rc;
+    rc = enqueue_forward_impl(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
+                              (hipStream_t)stream);
+    if (rc) c->counts_dirty = true; /* launched part of the chain */
+    return rc;
 }
 
 extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
@@ -628,7 +693,9 @@ extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int3
         drop_graph(c);
         HIP_TRY(c, hipStreamSynchronize(c->cap_stream));
         HIP_TRY(c, hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
-        rc = enqueue_forward(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, c->cap_stream);
+        /* captured, not run: a failure here leaves the counters untouched */
+        rc = enqueue_forward_impl(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
+                                  c->cap_stream);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(c->cap_stream, &g);
         if (rc) {
@@ -646,6 +713,8 @@ extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int3
         c->g_out = out;
         c->g_batch = batch;
     }
+    rc = clean_counts(c, (hipStream_t)stream);
+    if (rc) return rc;
     HIP_TRY(c, hipGraphLaunch(c->gexec, (hipStream_t)stream));
     return PRISM_OK;
 }

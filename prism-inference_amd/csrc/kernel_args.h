@@ -29,8 +29,19 @@ typedef struct AttnArgs {
     int32_t H, W;         /* token grid                                  */
     int32_t wx;           /* windows per row = ceil(W/8)                 */
     int32_t windows_per_frame;
-    int32_t* zero_counts; /* if set, workgroup 0 zeroes zero_n ints here  */
-    int32_t zero_n;       /* (the next router's counts, block chain only) */
+    /* fused routing (routed kernels only; the block chain's MoE blocks) */
+    const float* ln2_g;   /* [dim]                                       */
+    const float* ln2_b;   /* [dim]                                       */
+    const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts 0 */
+    const float* br;      /* [np]; entries >= n_experts are -inf          */
+    int32_t* assign;      /* [cap] expert id per token                    */
+    int32_t* counts;      /* expert e's total at counts[e * count_stride], zero on entry */
+    int32_t* perm;        /* [n_experts][cap] token ids bucketed by expert */
+    int32_t* zero_next;   /* if set, workgroup 0 clears zero_next[e * count_stride],
+                             e < n_experts: the next block's counters            */
+    int32_t n_experts;
+    int32_t cap;          /* tokens in the launch = batch * H * W         */
+    int32_t count_stride; /* ints between counters (a cache line apart in the chain) */
     int32_t pad_;
 } AttnArgs;
 
@@ -60,12 +71,12 @@ typedef struct ExpertArgs {
     const float* b1;      /* [n_experts][dim]                             */
     const uint16_t* w2;
     const float* b2;
-    const int32_t* counts; /* [n_experts]; NULL = dense stage (expert 0)  */
+    const int32_t* counts; /* counts[e * count_stride]; NULL = dense stage (expert 0) */
     const int32_t* perm;  /* [n_experts][cap]                             */
     int32_t n_tokens;
     int32_t n_experts;
     int32_t cap;
-    int32_t pad_;
+    int32_t count_stride;
 } ExpertArgs;
 
 #endif

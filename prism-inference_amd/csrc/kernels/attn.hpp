@@ -6,8 +6,9 @@
  * out-proj + fp16 residual :71-78) with the pre-LayerNorm added, as:
  *
  *  1. LN1 of the window's 64 slots -> xs (LDS, fp16). Padded slots are zero.
- *  2. Wave w owns heads w and w+4 (8-wave variant: head w). Per head, one MFMA GEMM pass over the
- *     model dim produces Q^T and K^T (rows = channel, cols = token) and V
+ *  2. Wave w owns heads w and w+4 (8-wave variant: head w). Per head, one
+ *     MFMA GEMM pass over the model dim produces Q^T and K^T (rows = channel,
+ *     cols = token) and V
  *     (rows = token, cols = channel), fp32 accumulate, bias, fp16 round.
  *  3. S^T = K Q^T is one MFMA per 16x16 tile straight from those registers:
  *     an accumulator lane holds 4 consecutive channels of one token, which is
@@ -17,18 +18,24 @@
  *     registers and O^T = V^T P^T is again register-to-register MFMA.
  *     O^T is normalised, rounded to fp16 and written to os (LDS).
  *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x (fp16 round), store.
+ *  5. Routed variants (NPT > 0, the block chain's MoE blocks) keep the output
+ *     tile in LDS and route it there: waves 0-3 each take 16 tokens through
+ *     LN2 + router GEMM + argmax (route_token, whose W_r fragments continue
+ *     the weight ring), then the window's counting sort (LDS histogram, one
+ *     global atomic per present expert, bucket scatter). This replaces the
+ *     router launch and its re-read of h.
  *
  * Weight streaming: every wave reads one fixed sequence of 1 KiB weight
- * fragments (head A's QKV k-steps, head B's, then the out-proj's) through a
+ * fragments (head A's QKV k-steps, head B's, the out-proj's, the router's) through a
  * register ring PF fragments deep, so loads run 2 k-steps ahead of the MFMAs
  * and the next head's and the out-proj's first fragments are in flight while
  * the softmax math runs. All workgroups read the same 0.5 MiB per block,
  * which stays L2-resident. Biases and LN parameters are staged in LDS once.
  */
 #pragma once
-#include "common.hpp"
+#include "route.hpp"
 
-template <int DIM, int HD, int NW>
+template <int DIM, int HD, int NW, int NPT>
 struct AttnShape {
     static constexpr int KS = DIM / 32;            /* k-steps over the model dim     */
     static constexpr int CT = HD / 16;             /* 16-channel tiles per head      */
@@ -37,17 +44,20 @@ struct AttnShape {
     static constexpr int HPW = 8 / NW;             /* heads per wave                 */
     static constexpr int ORT = DIM / 16 / NW;      /* out-proj row tiles per wave    */
     static constexpr int OUTF = KS * ORT;          /* out-proj fragments             */
-    static constexpr int TOTAL = HPW * HEADF + OUTF; /* fragment sequence length     */
+    static constexpr int RBASE = HPW * HEADF + OUTF; /* sequence length, no routing  */
+    static constexpr int TOTAL = RBASE + NPT * KS;   /* routing waves add W_r        */
     static constexpr int PF = 2 * FPK;             /* ring depth (2 k-steps ahead)   */
     static constexpr int LDS = DIM + 8;            /* padded LDS row, halfs          */
 };
 
-/* Fragment p of wave `wave`'s sequence: head A's QKV k-steps, head B's, then
- * the out-proj's (p is a compile-time constant or depends only on the head
- * index, so both branches are wave-uniform). */
-template <int DIM, int HD, int NW>
-__device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, int wave, int p, int loff) {
-    using S = AttnShape<DIM, HD, NW>;
+/* Fragment p of wave `wave`'s sequence: head A's QKV k-steps, head B's, the
+ * out-proj's, then (routing waves) the router's, k-step-major (p is a
+ * compile-time constant or depends only on the head index, so every branch
+ * is wave-uniform). */
+template <int DIM, int HD, int NW, int NPT>
+__device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, const FragSrc& wr, int wave, int p,
+                                        int loff) {
+    using S = AttnShape<DIM, HD, NW, NPT>;
     if (p < S::HPW * S::HEADF) {
         const int hh = p / S::HEADF, q = p % S::HEADF;
         const int ks = q / S::FPK, f = q % S::FPK;
@@ -56,16 +66,22 @@ __device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, 
         const int rt = (mat * DIM + h * HD) / 16 + c;
         return wqkv.load(rt * S::KS + ks, loff);
     }
-    const int q = p - S::HPW * S::HEADF;
-    const int ks = q / S::ORT, r = q % S::ORT;
-    return wo.load((wave * S::ORT + r) * S::KS + ks, loff);
+    if (NPT == 0 || p < S::RBASE) {
+        const int q = p - S::HPW * S::HEADF;
+        const int ks = q / S::ORT, r = q % S::ORT;
+        return wo.load((wave * S::ORT + r) * S::KS + ks, loff);
+    }
+    const int q = p - S::RBASE;
+    const int ks = q / (NPT > 0 ? NPT : 1), rt = q % (NPT > 0 ? NPT : 1);
+    return wr.load(rt * S::KS + ks, loff);
 }
 
-template <int DIM, int HD, int NW>
+template <int DIM, int HD, int NW, int NPT>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     static_assert(DIM / HD == 8, "8 heads");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    using S = AttnShape<DIM, HD, NW>;
+    static_assert(NPT >= 0 && NPT <= 4, "up to 64 experts");
+    using S = AttnShape<DIM, HD, NW, NPT>;
     constexpr int NT = 64 * NW;         /* threads                         */
     constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT, PF = S::PF;
     constexpr float LOG2E = 1.4426950408889634f;
@@ -76,8 +92,16 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     __shared__ __attribute__((aligned(16))) f16 os[64 * LDS];
     __shared__ float s_bqkv[3 * DIM];
     __shared__ float s_bo[DIM];
-    __shared__ float s_g[DIM];
+    __shared__ float s_g[DIM];          /* LN1, then LN2 (routing) */
     __shared__ float s_b[DIM];
+    /* routing scratch aliases the QKV biases, dead after the barrier ahead of
+     * the out-proj */
+    static_assert(3 * DIM >= 5 * 64, "routing scratch fits the QKV bias area");
+    float* const r_br = s_bqkv;                           /* [16*NPT] router bias    */
+    int* const r_hist = reinterpret_cast<int*>(s_bqkv) + 64; /* [64] window histogram */
+    int* const r_base = r_hist + 64;                     /* [64] bucket bases        */
+    int* const r_e = r_base + 64;                        /* [64] expert per slot     */
+    int* const r_rank = r_e + 64;                        /* [64] rank in its bucket  */
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -94,19 +118,22 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
 
     const FragSrc src_qkv(a.wqkv, 3u * DIM * DIM * 2u);
     const FragSrc src_o(a.wo, 1u * DIM * DIM * 2u);
+    const FragSrc src_r(NPT > 0 ? a.wr : a.wo, NPT > 0 ? 16u * NPT * DIM * 2u : 0u);
     const int loff = lane * 16;
+    /* waves 0-3 route tiles 0-3 of the window; only they stream W_r */
+    const bool routes = NPT > 0 && wave < 4;
+    const int total = routes ? S::TOTAL : S::RBASE;
 
     /* weight ring: first PF fragments go out before anything else */
     h8 ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p, loff);
+    for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p, loff);
     sched_fence();
 
-    /* block chain only: clear the counts the following router accumulates into
-     * (the previous expert stage, which read them, finished before this launch) */
-    if (a.zero_counts && blockIdx.x == 0)
-        for (int i = threadIdx.x; i < a.zero_n; i += NT) a.zero_counts[i] = 0;
-
+    /* block chain: clear the next block's counters (its previous reader, that
+     * block's expert stage of the previous chain, has finished) */
+    if (NPT > 0 && a.zero_next && blockIdx.x == 0 && threadIdx.x < a.n_experts)
+        a.zero_next[threadIdx.x * a.count_stride] = 0;
     for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
     for (int i = threadIdx.x; i < DIM; i += NT) {
         s_bo[i] = a.bo[i];
@@ -175,7 +202,8 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                     else if (mat == 1) accK[c][t] = mfma_16x16x32(w, xf[t], accK[c][t]);
                     else accV[t][c] = mfma_16x16x32(xf[t], w, accV[t][c]);
                 }
-                if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p + PF, loff);
+                if (p + PF < S::TOTAL && p + PF < total)
+                    ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
             }
             sched_fence();
         }
@@ -271,7 +299,18 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
         for (int r = 0; r < ORT; ++r)
             xin[t][r] = *reinterpret_cast<const h4*>(in + tbase[t] + (wave * ORT + r) * 16 + 4 * g);
     }
+    if constexpr (NPT > 0) {
+        /* LN1's parameters are dead (every wave passed the barrier after LN1) */
+        for (int i = threadIdx.x; i < DIM; i += NT) {
+            s_g[i] = a.ln2_g[i];
+            s_b[i] = a.ln2_b[i];
+        }
+    }
     __syncthreads();
+    if constexpr (NPT > 0) { /* the QKV biases are dead now */
+        for (int i = threadIdx.x; i < 16 * NPT; i += NT) r_br[i] = a.br[i];
+        if (threadIdx.x < 64) r_hist[threadIdx.x] = 0;
+    }
 
     /* ---- 4. out-proj + residual --------------------------------------- */
     f4 acc[ORT][4]; /* starts at the out-proj bias */
@@ -294,34 +333,82 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             const h8 w = ring[p % PF];
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
-            if (p + PF < S::TOTAL) ring[p % PF] = attn_frag<DIM, HD, NW>(src_qkv, src_o, wave, p + PF, loff);
+            if (p + PF < S::TOTAL && p + PF < total)
+                ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
         }
         sched_fence();
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        if (vt[t]) {
 #pragma unroll
-            for (int r = 0; r < ORT; ++r) {
-                const int ch = (wave * ORT + r) * 16 + 4 * g;
-                /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding) */
-                *reinterpret_cast<h4*>(out + tbase[t] + ch) = add_f16x4(cvt_h4(acc[r][t]), xin[t][r]);
+        for (int r = 0; r < ORT; ++r) {
+            const int ch = (wave * ORT + r) * 16 + 4 * g;
+            /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding) */
+            const h4 y = add_f16x4(cvt_h4(acc[r][t]), xin[t][r]);
+            if (vt[t]) *reinterpret_cast<h4*>(out + tbase[t] + ch) = y;
+            /* the tile stays on chip for routing; xs is free since the head loop */
+            if constexpr (NPT > 0) *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = y;
+        }
+    }
+
+    /* ---- 5. fused routing (moe_router.comp.glsl:24-52 + counting sort) -- */
+    if constexpr (NPT > 0) {
+        __syncthreads(); /* y tile complete in xs */
+        if (routes) {    /* wave w: tokens 16w..16w+15, all experts */
+            const int sl = 16 * wave + l16;
+            const int sy = wy * 8 + (sl >> 3), sx = wxx * 8 + (sl & 7);
+            h8 cur[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(xs + sl * LDS + 32 * ks + 8 * g);
+            const int e = route_token<DIM, NPT>(cur, s_g, s_b, r_br, g, a.n_experts, [&](int rt, int ks) {
+                const int p = S::RBASE + ks * NPT + rt;
+                const h8 w = ring[p % PF];
+                if (p + PF < S::TOTAL)
+                    ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
+                return w;
+            });
+            if (g == 0) {
+                r_e[sl] = e;
+                r_rank[sl] = (sy < a.H && sx < a.W) ? atomicAdd(&r_hist[e], 1) : 0;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < a.n_experts) {
+            const int c = r_hist[threadIdx.x];
+            r_base[threadIdx.x] = c ? atomicAdd(&a.counts[threadIdx.x * a.count_stride], c) : 0;
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int ty = wy * 8 + (threadIdx.x >> 3), tx = wxx * 8 + (threadIdx.x & 7);
+            if (ty < a.H && tx < a.W) {
+                const int token = frame * (a.H * a.W) + ty * a.W + tx;
+                const int e = r_e[threadIdx.x];
+                a.assign[token] = e;
+                const int slot = r_base[e] + r_rank[threadIdx.x];
+                if (slot < a.cap) a.perm[(int64_t)e * a.cap + slot] = token;
             }
         }
     }
 }
 
 /* 4 waves (2 heads each, 2 workgroups per CU) for large grids; 8 waves (one
- * head each, one workgroup per CU) when windows are scarcer than CUs. */
-extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d256(AttnArgs a) {
-    attn_window_body<256, 32, 4>(a);
-}
-extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128(AttnArgs a) {
-    attn_window_body<128, 16, 4>(a);
-}
-extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d256_w8(AttnArgs a) {
-    attn_window_body<256, 32, 8>(a);
-}
-extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d128_w8(AttnArgs a) {
-    attn_window_body<128, 16, 8>(a);
-}
+ * head each, one workgroup per CU) when windows are scarcer than CUs. The
+ * _r<NPT> kernels also route the window's tokens (16*NPT padded experts). */
+#define PRISM_ATTN_KERNELS(D, HD, NPT, SUF)                                                          \
+    extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d##D##SUF(AttnArgs a) {          \
+        attn_window_body<D, HD, 4, NPT>(a);                                                          \
+    }                                                                                                \
+    extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d##D##_w8##SUF(AttnArgs a) {     \
+        attn_window_body<D, HD, 8, NPT>(a);                                                          \
+    }
+PRISM_ATTN_KERNELS(256, 32, 0, )
+PRISM_ATTN_KERNELS(256, 32, 1, _r1)
+PRISM_ATTN_KERNELS(256, 32, 2, _r2)
+PRISM_ATTN_KERNELS(256, 32, 3, _r3)
+PRISM_ATTN_KERNELS(256, 32, 4, _r4)
+PRISM_ATTN_KERNELS(128, 16, 0, )
+PRISM_ATTN_KERNELS(128, 16, 1, _r1)
+PRISM_ATTN_KERNELS(128, 16, 2, _r2)
+PRISM_ATTN_KERNELS(128, 16, 3, _r3)
+PRISM_ATTN_KERNELS(128, 16, 4, _r4)
+#undef PRISM_ATTN_KERNELS

@@ -32,14 +32,17 @@
 #pragma once
 #include "common.hpp"
 
-template <int DIM, int BM>
+template <int DIM, int BM, int NW>
 __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int NT = 64 * NW;   /* threads                          */
     constexpr int KS = DIM / 32;
     constexpr int LDS = DIM + 8;
     constexpr int TT = BM / 16;   /* token tiles per workgroup        */
-    constexpr int RT = DIM / 64;  /* 16-row output tiles per wave     */
+    constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave */
     constexpr int LPS = DIM / 16; /* LN lanes per row                 */
     constexpr int RPI = 64 / LPS; /* LN rows per wave iteration       */
+    static_assert(RT >= 1 && BM % (NW * RPI) == 0, "tile shape");
 
     __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, then GELU output */
     __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
@@ -57,7 +60,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (wave == 0) {
         if (a.counts) {
-            const int c = lane < a.n_experts ? min(a.counts[lane], a.cap) : 0;
+            const int c = lane < a.n_experts ? min(a.counts[lane * a.count_stride], a.cap) : 0;
             const int nt = (c + BM - 1) / BM;
             int incl = nt;
 #pragma unroll
@@ -81,7 +84,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             sh_rows = min(BM, a.n_tokens - row0);
         }
     } else {
-        for (int i = threadIdx.x - 64; i < DIM; i += 192) {
+        for (int i = threadIdx.x - 64; i < DIM; i += NT - 64) {
             s_g[i] = a.ln_g[i];
             s_b[i] = a.ln_b[i];
         }
@@ -95,11 +98,11 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
         const int loff = lane * 16;
 
-        for (int i = threadIdx.x; i < DIM; i += 256) {
+        for (int i = threadIdx.x; i < DIM; i += NT) {
             s_b1[i] = a.b1[(int64_t)e * DIM + i];
             s_b2[i] = a.b2[(int64_t)e * DIM + i];
         }
-        for (int r = threadIdx.x; r < BM; r += 256) {
+        for (int r = threadIdx.x; r < BM; r += NT) {
             int t = -1;
             if (r < rows) {
                 t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
@@ -112,12 +115,12 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         /* the gathered rows' loads go out first, then every W1 fragment of
          * this wave's rows, then LN2 runs on the rows while W1 arrives
          * (loads retire in issue order) */
-        constexpr int IT = BM / 4 / RPI;
+        constexpr int IT = BM / NW / RPI;
         RowChunk rc[IT];
         int rt_tok[IT];
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
-            rt_tok[it] = tok[wave * (BM / 4) + it * RPI + lane / LPS];
+            rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
             rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM, rt_tok[it] >= 0);
         }
         h8 wf[RT][KS];
@@ -128,7 +131,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         sched_fence();
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
-            const int r = wave * (BM / 4) + it * RPI + lane / LPS;
+            const int r = wave * (BM / NW) + it * RPI + lane / LPS;
             ln_store<DIM>(rc[it], rt_tok[it] >= 0, s_g, s_b, xs + r * LDS, hs + r * LDS);
         }
         __syncthreads();
@@ -207,9 +210,17 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 
 }
 
+/* 4 waves (2 workgroups per CU) for large grids; 8 waves (each streaming half
+ * as many weight rows) when tiles are scarcer than CUs. */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm64(ExpertArgs a) {
-    expert_body<256, 64>(a);
+    expert_body<256, 64, 4>(a);
 }
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm64(ExpertArgs a) {
-    expert_body<128, 64>(a);
+    expert_body<128, 64, 4>(a);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d256_bm64_w8(ExpertArgs a) {
+    expert_body<256, 64, 8>(a);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d128_bm64_w8(ExpertArgs a) {
+    expert_body<128, 64, 8>(a);
 }

@@ -3,17 +3,18 @@
  * the host engine with hipModuleLoad and launched with hipModuleLaunchKernel.
  *
  * Kernels (extern "C" names, one per stage and supported shape):
- *   prism_attn_d256 / prism_attn_d128              attention stage
- *   prism_router_d256 / prism_router_d128          router + counting sort
+ *   prism_attn_d{256,128}[_w8]                     attention stage (4 or 8 waves)
+ *   prism_attn_d{256,128}[_w8]_r{1..4}             attention + fused routing
+ *   prism_router_d{256,128}_n{1..4}                router + counting sort
  *   prism_expert_d{256,128}_bm64                   grouped expert FFN
- *   prism_zero_i32                                 clears the router counts
+ *   prism_zero_i32                                 clears routing counters
  */
 #include "attn.hpp"
 #include "router.hpp"
 #include "expert.hpp"
 
-/* The router stage's counts must start at zero; a kernel (not a memset node)
- * keeps the launch safe under stream capture. */
+/* Routing counters must start at zero; a kernel (not a memset node) keeps
+ * the launch safe under stream capture. */
 extern "C" __global__ void __launch_bounds__(256) prism_zero_i32(int32_t* p, int32_t n) {
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
 }

@@ -1,0 +1,111 @@
+/*
+ * route.hpp - per-token routing math shared by the router stage and the
+ * attention kernel's fused routing epilogue.
+ *
+ * Restates shaders/moe_router.comp.glsl:24-52 widened to N logits
+ * (moe_ffn_16exp.comp.glsl:27-34): hn = LN2(h), logits = r16(W_r hn + b_r),
+ * expert = first index of the maximum (strict >, moe_router.comp.glsl:42-45).
+ *
+ * Lane layout (one 16-token tile per wave): lane (g = lane >> 4, l16 = lane & 15)
+ * holds channels 32*ks + 8*g .. +7 of token l16 in cur[ks], which is exactly
+ * the B-operand fragment of logits^T = W_r * hn^T, so the LayerNorm runs in
+ * registers and feeds the MFMAs directly. Element i of row tile rt of the
+ * result is expert 16*rt + 4*g + i of token l16. Every split of the work
+ * below (whole tokens per wave, or one row tile per wave with the partial
+ * maxima merged in row-tile order) gives the same expert: the maximum fp16
+ * logit, lowest id among ties.
+ */
+#pragma once
+#include "common.hpp"
+
+/* hn = r16(LN2(h)) in the same lane layout as cur (the B operand of the
+ * router GEMM). */
+template <int DIM>
+__device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b, int g,
+                                         h8 (&hn)[DIM / 32]) {
+    constexpr int KS = DIM / 32;
+    float s = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += (float)cur[ks][j];
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    const float mean = s * (1.0f / DIM);
+    float q = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float t = (float)cur[ks][j] - mean;
+            q = __builtin_fmaf(t, t, q);
+        }
+    q += __shfl_xor(q, 16, 64);
+    q += __shfl_xor(q, 32, 64);
+    const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        asm volatile("" ::: "memory"); /* keep this k-step's gamma/beta reads here */
+#pragma unroll
+        for (int j = 0; j < 8; j += 4) {
+            f4 t;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = 32 * ks + 8 * g + j + i;
+                t[i] = __builtin_fmaf((float)cur[ks][j + i] - mean, inv * s_g[c], s_b[c]);
+            }
+            const h4 q4 = cvt_h4(t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hn[ks][j + i] = q4[i];
+        }
+    }
+}
+
+/* Best (fp16-rounded logit, expert) of one 16-expert row tile rt for the
+ * token of this lane's column: 4 values in-lane, then the 4 lane groups.
+ * Larger logit wins, ties go to the lower id; a tile with no finite logit
+ * returns (-3e38, INT_MAX). */
+__device__ __forceinline__ void route_tile_best(const f4& acc, int rt, int g, float& best_v, int& best_e) {
+    const h4 lg = cvt_h4(acc); /* logits are fp16 values */
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lv = (float)lg[i];
+        if (lv > best_v) { best_v = lv; best_e = 16 * rt + 4 * g + i; }
+    }
+}
+
+__device__ __forceinline__ void route_combine_groups(float& best_v, int& best_e) {
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) {
+        const float ov = __shfl_xor(best_v, m, 64);
+        const int oe = __shfl_xor(best_e, m, 64);
+        if (ov > best_v || (ov == best_v && oe < best_e)) { best_v = ov; best_e = oe; }
+    }
+}
+
+/* frag(rt, ks) returns router fragment (row tile rt, k-step ks) of the packed
+ * W_r. s_br holds 16*NPT biases with -inf past the real experts. Returns the
+ * token's expert in all 4 lane groups of its column. */
+template <int DIM, int NPT, class Frag>
+__device__ __forceinline__ int route_token(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
+                                           const float* s_br, int g, int n_experts, Frag&& frag) {
+    constexpr int KS = DIM / 32;
+    h8 hn[KS];
+    route_ln<DIM>(cur, s_g, s_b, g, hn);
+    f4 acc[NPT]; /* starts at the router bias */
+#pragma unroll
+    for (int rt = 0; rt < NPT; ++rt)
+        acc[rt] = f4{s_br[16 * rt + 4 * g], s_br[16 * rt + 4 * g + 1], s_br[16 * rt + 4 * g + 2],
+                     s_br[16 * rt + 4 * g + 3]};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < NPT; ++rt) acc[rt] = mfma_16x16x32(frag(rt, ks), hn[ks], acc[rt]);
+    float best_v = -3.0e38f;
+    int best_e = 0x7fffffff;
+#pragma unroll
+    for (int rt = 0; rt < NPT; ++rt) route_tile_best(acc[rt], rt, g, best_v, best_e);
+    route_combine_groups(best_v, best_e);
+    if (best_e >= n_experts || best_e < 0) best_e = 0; /* non-finite logits */
+    return best_e;
+}

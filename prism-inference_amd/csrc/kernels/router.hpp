@@ -3,10 +3,10 @@
  *
  * Restates shaders/moe_router.comp.glsl:24-52 widened to N logits
  * (moe_ffn_16exp.comp.glsl:27-34 is the N-wide form the reference intended):
- * logits = r16(W_r LN2(h) + b_r), first max wins (strict >, :42-45), the
- * expert id is written per token (:48) and the per-expert count is
- * incremented (:51). The count atomics become a workgroup-local LDS
- * histogram plus one global atomic per (workgroup, expert); each token's LDS
+ * the per-token math (route_token, route.hpp) gives the expert, the expert id
+ * is written per token (:48) and the per-expert count is incremented (:51).
+ * The count atomics become a workgroup-local LDS histogram plus one global
+ * atomic per (workgroup, expert); each token's LDS
  * rank then places it in its expert's bucket of `perm`, which is the
  * expert-contiguous segment the grouped expert GEMM consumes.
  *
@@ -24,7 +24,7 @@
  * per CU.
  */
 #pragma once
-#include "common.hpp"
+#include "route.hpp"
 
 #define ROUTER_MAX_TILES_PER_WAVE 8
 
@@ -79,71 +79,8 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
         for (int ks = 0; ks < KS; ++ks) cur[ks] = xr[ks];
         if (it + 1 < tpw) router_load_tile<DIM, KS>(a, token + 16, g, xr); /* next tile in flight */
 
-        /* LN2 in registers: this lane holds channels 32ks + 8g + j */
-        float s = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += (float)cur[ks][j];
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
-        const float mean = s * (1.0f / DIM);
-        float q = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float t = (float)cur[ks][j] - mean;
-                q = __builtin_fmaf(t, t, q);
-            }
-        q += __shfl_xor(q, 16, 64);
-        q += __shfl_xor(q, 32, 64);
-        const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
-
-        /* logits^T: element i of row tile rt = expert 16rt+4g+i, token l16 */
-        f4 acc[NPT];
-#pragma unroll
-        for (int rt = 0; rt < NPT; ++rt)
-            acc[rt] = f4{s_br[16 * rt + 4 * g], s_br[16 * rt + 4 * g + 1], s_br[16 * rt + 4 * g + 2],
-                         s_br[16 * rt + 4 * g + 3]};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            asm volatile("" ::: "memory"); /* keep this k-step's gamma/beta reads here */
-            h8 hn;
-#pragma unroll
-            for (int j = 0; j < 8; j += 4) {
-                f4 t;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int c = 32 * ks + 8 * g + j + i;
-                    t[i] = __builtin_fmaf((float)cur[ks][j + i] - mean, inv * s_g[c], s_b[c]);
-                }
-                const h4 q4 = cvt_h4(t);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) hn[j + i] = q4[i];
-            }
-#pragma unroll
-            for (int rt = 0; rt < NPT; ++rt) acc[rt] = mfma_16x16x32(s_wr[(rt * KS + ks) * 64 + lane], hn, acc[rt]);
-        }
-        float best_v = -3.0e38f;
-        int best_e = 0x7fffffff;
-#pragma unroll
-        for (int rt = 0; rt < NPT; ++rt) {
-            const h4 lg = cvt_h4(acc[rt]); /* logits are fp16 values */
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float lv = (float)lg[i];
-                if (lv > best_v) { best_v = lv; best_e = 16 * rt + 4 * g + i; }
-            }
-        }
-        /* combine the 4 lane groups: larger logit wins, ties go to the lower id */
-#pragma unroll
-        for (int m = 16; m <= 32; m <<= 1) {
-            const float ov = __shfl_xor(best_v, m, 64);
-            const int oe = __shfl_xor(best_e, m, 64);
-            if (ov > best_v || (ov == best_v && oe < best_e)) { best_v = ov; best_e = oe; }
-        }
-        if (best_e >= a.n_experts || best_e < 0) best_e = 0; /* non-finite logits */
+        const int best_e = route_token<DIM, NPT>(cur, s_g, s_b, s_br, g, a.n_experts,
+                                                 [&](int rt, int ks) { return s_wr[(rt * KS + ks) * 64 + lane]; });
         if (g == 0) {
             s_e[local] = best_e;
             s_rank[local] = token < a.n_tokens ? atomicAdd(&hist[best_e], 1) : 0;

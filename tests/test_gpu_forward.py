@@ -62,6 +62,68 @@ def test_graph_replay_matches_eager(hip, engine, device_arena, name, nb, H, W, b
         hip.sync()
 
 
+# MoE shapes the presets do not cover: 40 experts (3 router row tiles, 24
+# padded) and a d128 MoE model (8 heads x 16, 2 row tiles)
+EXTRA = {
+    "moe40": P.Config("moe40", 256, 2, 8, 32, 40, 68, 120, 1, P.ROUTE_UNIFORM),
+    "moe24d128": P.Config("moe24d128", 128, 3, 8, 16, 24, 68, 120, 1, P.ROUTE_ZIPF),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,nb,H,W,batch", [
+    ("moe64", 3, 68, 120, 1),      # 8-wave routed kernel, 4 router row tiles
+    ("moe64", 2, 68, 120, 4),      # 4-wave routed kernel (540 windows)
+    ("moe16", 2, 20, 28, 3),       # 1 row tile, ragged windows, 3 frames
+    ("moe16", 1, 20, 28, 2),       # one block: its counters are cleared inside the chain
+    ("moe40", 2, 68, 120, 1),
+    ("moe40", 2, 68, 120, 4),
+    ("moe24d128", 3, 68, 120, 1),
+    ("moe24d128", 2, 68, 120, 4),
+])
+def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch):
+    """The chain routes inside the attention kernel; the stage calls run the
+    separate router. Same fp16 inputs and the same arithmetic order, so the
+    expert of every token and the block outputs must be identical."""
+    cfg = EXTRA[name] if name in EXTRA else P.CONFIGS[name]
+    desc = cfg.desc(n_blocks=nb, H=H, W=W)
+    blob, offs = P.synth_weights(desc, seed=3, routing=cfg.routing)
+    engine.load_weights(desc, blob, offs)
+    n, d, N = batch * H * W, cfg.dim, cfg.n_experts
+    x = P.synth_features(cfg, batch=batch, H=H, W=W, seed=9).reshape(n, d)
+    dx, dy = device_arena(n * d * 2), device_arena(n * d * 2)
+    hip.upload(dx.ptr, x)
+    print(f"[chain] {name} {nb} blocks {H}x{W} batch {batch}", flush=True)
+    for _ in range(2):  # the second chain starts from the counters the first one left
+        engine.forward(dx.ptr, dy.ptr, batch)
+    hip.sync()
+    y_chain = hip.download(np.empty(n * d, np.uint16), dy.ptr)
+    a_ptr, ntok = engine.forward_assignments()
+    assert ntok == n
+    a_chain = hip.download(np.empty(nb * n, np.int32), a_ptr).reshape(nb, n)
+
+    feats = device_arena(3 * n * d * 2)
+    aux = device_arena(P.aux_elems(N, n) * 4)
+    a_off, c_off, p_off = 0, n, n + N
+    hip.upload(feats.ptr, x)
+    cur, nxt = 0, 2 * n * d
+    for b in range(nb):
+        assert engine.attn(engine.attn_push(b, cur, n * d, H, W), feats.ptr, batch) == 0, engine.error()
+        assert engine.router(engine.router_push(b, H * W, n * d, a_off, c_off, p_off), feats.ptr, aux.ptr,
+                             batch) == 0, engine.error()
+        push = engine.expert_push(b, H * W, n * d, nxt, a_off, c_off, p_off)
+        assert engine.experts(push, feats.ptr, aux.ptr, batch) == 0, engine.error()
+        hip.sync()
+        a_stage = hip.download(np.empty(n, np.int32), aux.ptr)
+        diff = int((a_stage != a_chain[b]).sum())
+        print(f"[chain] {name} block {b}: {diff} assignments differ; load max share "
+              f"{np.bincount(a_stage, minlength=N).max() / n:.3f}")
+        assert diff == 0, f"block {b}"
+        cur, nxt = nxt, cur
+    y_stage = hip.download(np.empty(n * d, np.uint16), feats.ptr + cur * 2)
+    assert (y_stage == y_chain).all(), f"{int((y_stage != y_chain).sum())} output values differ"
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,H,W,batch", [
     ("moe64", 4, 68, 120, 1),

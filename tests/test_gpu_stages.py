@@ -139,7 +139,12 @@ def test_router_then_experts(hip, engine, device_arena, name, H, W, batch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,H,W,batch", [("std256", 68, 120, 1), ("dense128", 68, 120, 2), ("std256", 5, 7, 1)])
+@pytest.mark.parametrize("name,H,W,batch", [
+    ("std256", 68, 120, 1),      # 128 tiles: 8-wave kernel
+    ("dense128", 68, 120, 2),
+    ("std256", 5, 7, 1),         # one partial tile
+    ("std256", 68, 120, 4),      # 512 tiles: 4-wave kernel
+])
 def test_dense_ffn_stage(hip, engine, device_arena, name, H, W, batch):
     cfg = P.CONFIGS[name]
     desc, blob, offs, w = make_model(cfg, 1, H, W)
