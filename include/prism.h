@@ -200,6 +200,54 @@ int prism_forward_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch
 int prism_forward_assignments(prism_ctx* ctx, const int32_t** assign_dev,
                               int64_t* tokens_per_block);
 
+/* ---- projection adapters (either side of the block chain) --------------- */
+
+/* Element offsets of the two adapters in an fp16 blob: the reference's
+ * end-to-end layout (prism_moe_bench.cpp:351-352) proj_up_w [dim][in_dim],
+ * proj_up_b [dim], proj_dn_w [in_dim][dim], proj_dn_b [in_dim]. in_dim is the
+ * encoder's channel count (128). */
+typedef struct prism_adapter_offsets {
+    int32_t in_dim, pad_;
+    int64_t up_w, up_b, down_w, down_b;
+} prism_adapter_offsets;
+
+/* Projection stage parameters: shaders/pw_project_128to256.comp.glsl:11-15 and
+ * shaders/pw_project_256to128.comp.glsl:9-13 {n_tokens, w_offset, b_offset,
+ * input_offset, output_offset}. n_tokens is per frame; the weight offsets must
+ * name the loaded adapter. */
+typedef struct prism_project_push {
+    int32_t n_tokens, pad_;
+    int64_t w_offset, b_offset, input_offset, output_offset;
+} prism_project_push;
+
+/* Place the adapters in a blob from element `base` on (8-element aligned,
+ * the reference's wa() order); *end = first element past them. Host only. */
+int prism_adapter_layout(const prism_model_desc* desc, int32_t in_dim, int64_t base,
+                         prism_adapter_offsets* offs, int64_t* end);
+
+/* Upload both adapters (host fp16 blob, `bytes` long) for the loaded model's
+ * dim; in_dim 128. Loading weights of another dim drops them. */
+int prism_load_adapters(prism_ctx* ctx, const void* blob, size_t bytes,
+                        const prism_adapter_offsets* offs);
+
+/* pw_project_128to256 (shaders/pw_project_128to256.comp.glsl:20-40):
+ * out = ReLU(r16(W_up x + b_up)), in_dim -> dim channels per token.
+ * pw_project_256to128 (shaders/pw_project_256to128.comp.glsl:20-33):
+ * out = r16(W_down x + b_down), dim -> in_dim. One launch each. */
+int prism_project_up(prism_ctx* ctx, const prism_project_push* p, void* features,
+                     int32_t batch, void* stream);
+int prism_project_down(prism_ctx* ctx, const prism_project_push* p, void* features,
+                       int32_t batch, void* stream);
+
+/* The transformer section of the reference's end-to-end frame
+ * (prism_moe_bench.cpp:408-444): up-projection, every block, down-projection.
+ * in and out: device fp16 [batch][H*W][in_dim] (in is not modified).
+ * _graph replays a captured hipGraph like prism_forward_graph. */
+int prism_forward_adapted(prism_ctx* ctx, const void* in, void* out, int32_t batch,
+                          void* stream);
+int prism_forward_adapted_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch,
+                                void* stream);
+
 /* aux arena size in int32 elements that a router + expert pair needs for
  * n_experts experts and batch*n_tokens tokens when laid out as
  * [assignment | counts | perm]. */

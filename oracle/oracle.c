@@ -379,6 +379,27 @@ int oracle_expert_stage(const oracle_cfg* c, const float* w, const oracle_block_
 
 /* prism_moe_bench.cpp:414-438: per block attn -> router -> experts, then the
  * output feeds the next block. The input is left untouched here. */
+/* Projection adapters around the block chain (vulkan_engine/prism_moe_bench.cpp:408-444):
+ * shaders/pw_project_128to256.comp.glsl:25-37 (relu = 1) and
+ * shaders/pw_project_256to128.comp.glsl:25-32 (relu = 0). Per token,
+ * y = r16(W x + b) (coopVecMatMulAddNV's fp16 result), then for the up
+ * projection y = r16(max(float(y), 0)), which is exact. W is [out_dim][in_dim]
+ * row-major. */
+int oracle_project(const float* W, const float* b, int in_dim, int out_dim, int relu, const float* x,
+                   int n, int faithful, float* y) {
+    if (!W || !b || !x || !y || n < 0 || in_dim <= 0 || out_dim <= 0 || in_dim % 8) return -1;
+    const int chunk = 64;
+#pragma omp parallel for schedule(dynamic)
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        const int m = n - t0 < chunk ? n - t0 : chunk;
+        float* yy = y + (size_t)t0 * out_dim;
+        gemm_xwT(x + (size_t)t0 * in_dim, m, in_dim, W, b, out_dim, yy, out_dim, faithful);
+        if (relu)
+            for (size_t i = 0; i < (size_t)m * out_dim; ++i) yy[i] = yy[i] > 0.f ? yy[i] : 0.f;
+    }
+    return 0;
+}
+
 int oracle_forward(const oracle_cfg* c, const float* w, const oracle_block_offsets* offs,
                    int n_blocks, const float* x, float* y, int32_t* assign_out, float* h_out) {
     if (check_cfg(c) || !w || !offs || !x || !y || n_blocks <= 0) return -1;

@@ -11,6 +11,8 @@
  *   shaders/moe_router.comp.glsl:24-52            router stage (N-wide)
  *   shaders/moe_ffn_16exp.comp.glsl:27-34         intended N-wide argmax
  *   shaders/moe_expert_skip.comp.glsl:25-54       expert stage
+ *   shaders/pw_project_128to256.comp.glsl:25-37   projection 128 -> 256 + ReLU
+ *   shaders/pw_project_256to128.comp.glsl:25-32   projection 256 -> 128
  *   vulkan_engine/prism_moe_bench.cpp:164-172     weight offset layout
  *   vulkan_engine/prism_moe_bench.cpp:262-291     per-block host order
  *
@@ -81,6 +83,12 @@ int oracle_expert_stage(const oracle_cfg* c, const float* w,
 int oracle_forward(const oracle_cfg* c, const float* w,
                    const oracle_block_offsets* offs, int n_blocks,
                    const float* x, float* y, int32_t* assign_out, float* h_out);
+
+/* Projection adapter (pw_project_128to256 with relu = 1, pw_project_256to128
+ * with relu = 0): y[t] = r16(W x[t] + b), then max(y, 0) if relu.
+ * W is [out_dim][in_dim]; in_dim % 8 == 0. */
+int oracle_project(const float* W, const float* b, int in_dim, int out_dim, int relu, const float* x,
+                   int n, int faithful, float* y);
 
 int oracle_max_threads(void);
 void oracle_set_threads(int n);

@@ -48,6 +48,7 @@ def lib():
         L.oracle_forward.argtypes = [C.POINTER(Cfg), _F, C.POINTER(Offs), C.c_int, _F, _F, _I, _F]
         L.oracle_layernorm.argtypes = [_F, _F, _F, C.c_int, C.c_int, C.c_int, _F]
         L.oracle_gelu.argtypes = [_F, _F, C.c_size_t]
+        L.oracle_project.argtypes = [_F, _F, C.c_int, C.c_int, C.c_int, _F, C.c_int, C.c_int, _F]
         L.oracle_window_attention.argtypes = [C.POINTER(Cfg), _F, _F, _F, _F]
         L.oracle_f16_to_f32.argtypes = [C.POINTER(C.c_uint16), _F, C.c_size_t]
         L.oracle_f32_to_f16.argtypes = [_F, C.POINTER(C.c_uint16), C.c_size_t]
@@ -137,6 +138,20 @@ def forward(c: Cfg, w: np.ndarray, offs_list, x: np.ndarray, keep_h: bool = Fals
     _chk(lib().oracle_forward(C.byref(c), _f(w), arr, nb, _f(x), _f(y), _i(assign),
                               _f(h) if keep_h else None), "oracle_forward")
     return y, assign, h
+
+
+def project(W: np.ndarray, b: np.ndarray, x: np.ndarray, relu: bool, faithful: bool = True) -> np.ndarray:
+    """Projection adapter: y = r16(W x + b) per token (+ ReLU for the up
+    projection). W [out][in], x [n][in] (float32, fp16-representable)."""
+    W = np.ascontiguousarray(W, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out_dim, in_dim = W.shape
+    assert x.shape[1] == in_dim and b.shape == (out_dim,)
+    y = np.empty((x.shape[0], out_dim), np.float32)
+    _chk(lib().oracle_project(_f(W), _f(b), in_dim, out_dim, int(relu), _f(x), x.shape[0], int(faithful), _f(y)),
+         "oracle_project")
+    return y
 
 
 def layernorm(x: np.ndarray, g: np.ndarray, b: np.ndarray, round16: bool = False) -> np.ndarray:

@@ -60,6 +60,7 @@ struct prism_ctx {
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
     hipFunction_t f_zero = nullptr;
+    hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */
     std::string err;
 
     bool loaded = false;
@@ -67,11 +68,19 @@ struct prism_ctx {
     void* warena = nullptr;
     std::vector<DevBlock> blocks;
 
+    /* projection adapters (prism_load_adapters) */
+    void* aarena = nullptr;
+    bool adapters = false;
+    prism_adapter_offsets aoffs{};
+    uint16_t *up_w = nullptr, *down_w = nullptr; /* packed */
+    float *up_b = nullptr, *down_b = nullptr;
+
     /* forward workspace */
     void* ws = nullptr;
     int ws_batch = 0;
     uint16_t* ws_attn = nullptr;
     uint16_t* ws_scratch = nullptr;
+    uint16_t* ws_io[2] = {};      /* adapted chain: projected input / chain output */
     int32_t* ws_assign = nullptr; /* [n_blocks][n] */
     int32_t* ws_counts = nullptr; /* [n_blocks][N][CHAIN_COUNT_STRIDE] */
     int32_t* ws_perm = nullptr;   /* [N][n] */
@@ -85,6 +94,7 @@ struct prism_ctx {
     const void* g_in = nullptr;
     void* g_out = nullptr;
     int g_batch = 0;
+    bool g_adapted = false;
 };
 
 static int fail(prism_ctx* c, int code, const char* fmt, ...) {
@@ -153,6 +163,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_expert[0][0], "prism_expert_d128_bm64"},  {&c->f_expert[1][0], "prism_expert_d256_bm64"},
         {&c->f_expert[0][1], "prism_expert_d128_bm64_w8"}, {&c->f_expert[1][1], "prism_expert_d256_bm64_w8"},
         {&c->f_zero, "prism_zero_i32"},
+        {&c->f_proj[0][0], "prism_project_up_d128"},   {&c->f_proj[0][1], "prism_project_down_d128"},
+        {&c->f_proj[1][0], "prism_project_up_d256"},   {&c->f_proj[1][1], "prism_project_down_d256"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);
@@ -188,11 +200,21 @@ static void drop_graph(prism_ctx* c) {
     c->g_in = nullptr;
     c->g_out = nullptr;
     c->g_batch = 0;
+    c->g_adapted = false;
+}
+
+static void drop_adapters(prism_ctx* c) {
+    if (c->aarena) (void)hipFree(c->aarena);
+    c->aarena = nullptr;
+    c->adapters = false;
+    c->up_w = c->down_w = nullptr;
+    c->up_b = c->down_b = nullptr;
 }
 
 static void drop_workspace(prism_ctx* c) {
     if (c->ws) (void)hipFree(c->ws);
     c->ws = nullptr;
+    c->ws_io[0] = c->ws_io[1] = nullptr;
     c->ws_batch = 0;
     c->ws_tokens = 0;
 }
@@ -203,6 +225,7 @@ extern "C" void prism_destroy(prism_ctx* c) {
     (void)hipDeviceSynchronize();
     drop_graph(c);
     drop_workspace(c);
+    drop_adapters(c);
     if (c->warena) (void)hipFree(c->warena);
     if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
     if (c->module) (void)hipModuleUnload(c->module);
@@ -340,6 +363,7 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
     if (c->desc.n_experts != d->n_experts || c->desc.dim != d->dim || c->desc.n_blocks != d->n_blocks ||
         c->desc.spatial_h != d->spatial_h || c->desc.spatial_w != d->spatial_w)
         drop_workspace(c);
+    if (c->desc.dim != d->dim) drop_adapters(c);
     c->desc = *d;
     c->loaded = true;
     return PRISM_OK;
@@ -361,6 +385,50 @@ extern "C" int prism_load_weights_file(prism_ctx* c, const prism_model_desc* d, 
     }
     if (size > 0 && !f.read(data.data(), size)) return fail(c, PRISM_ERR_INVALID, "short read on %s", path);
     return prism_load_weights(c, d, data.data(), data.size(), offs);
+}
+
+extern "C" int prism_load_adapters(prism_ctx* c, const void* blob, size_t bytes, const prism_adapter_offsets* a) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "load the model weights before the adapters");
+    if (!blob) return fail(c, PRISM_ERR_INVALID, "adapter blob is NULL");
+    if (bytes % 2) return fail(c, PRISM_ERR_BLOB, "blob size %zu is not a whole number of fp16 values", bytes);
+    std::string why;
+    const int rc = validate_adapters(&c->desc, a, (int64_t)(bytes / 2), &why);
+    if (rc) return fail(c, rc, "%s", why.c_str());
+    HIP_TRY(c, hipSetDevice(c->device));
+    const int D = c->desc.dim, I = a->in_dim;
+    const uint16_t* src = static_cast<const uint16_t*>(blob);
+    Arena ar;
+    const size_t o_uw = ar.take((size_t)D * I * 2), o_ub = ar.take((size_t)D * 4);
+    const size_t o_dw = ar.take((size_t)I * D * 2), o_db = ar.take((size_t)I * 4);
+    std::vector<uint8_t> host(ar.off, 0);
+    pack_fragments(src + a->up_w, D, I, D, reinterpret_cast<uint16_t*>(host.data() + o_uw));
+    pack_fragments(src + a->down_w, I, D, I, reinterpret_cast<uint16_t*>(host.data() + o_dw));
+    float* ub = reinterpret_cast<float*>(host.data() + o_ub);
+    float* db = reinterpret_cast<float*>(host.data() + o_db);
+    for (int i = 0; i < D; ++i) ub[i] = half_to_float(src[a->up_b + i]);
+    for (int i = 0; i < I; ++i) db[i] = half_to_float(src[a->down_b + i]);
+
+    (void)hipDeviceSynchronize();
+    drop_graph(c);
+    drop_adapters(c);
+    void* arena = nullptr;
+    hipError_t e = hipMalloc(&arena, ar.off);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for adapters: %s", ar.off, hipGetErrorString(e));
+    e = hipMemcpy(arena, host.data(), ar.off, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(arena);
+        return fail(c, PRISM_ERR_HIP, "adapter upload: %s", hipGetErrorString(e));
+    }
+    uint8_t* b = static_cast<uint8_t*>(arena);
+    c->aarena = arena;
+    c->up_w = reinterpret_cast<uint16_t*>(b + o_uw);
+    c->up_b = reinterpret_cast<float*>(b + o_ub);
+    c->down_w = reinterpret_cast<uint16_t*>(b + o_dw);
+    c->down_b = reinterpret_cast<float*>(b + o_db);
+    c->aoffs = *a;
+    c->adapters = true;
+    return PRISM_OK;
 }
 
 /* ------------------------------------------------------------ launches */
@@ -481,6 +549,19 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     return launch(c, c->f_expert[dim_index(D)][w8], (unsigned)tiles, a, s, w8 ? 512u : 256u);
 }
 
+/* up: in_dim -> dim with ReLU; down: dim -> in_dim. n tokens. */
+int enqueue_project(prism_ctx* c, bool up, const uint16_t* in, uint16_t* out, int64_t n, hipStream_t s) {
+    ProjArgs a{};
+    a.in = in;
+    a.out = out;
+    a.w = up ? c->up_w : c->down_w;
+    a.b = up ? c->up_b : c->down_b;
+    a.n_tokens = n;
+    const int64_t grid = (n + 63) / 64;
+    if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "projection grid %lld out of range", (long long)grid);
+    return launch(c, c->f_proj[dim_index(c->desc.dim)][up ? 0 : 1], (unsigned)grid, a, s);
+}
+
 /* which: 0 = attention (qkv_w), 1 = router (router_w), 2 = experts (exp_w1) */
 const DevBlock* find_block(prism_ctx* c, int64_t key, int which) {
     for (const DevBlock& k : c->blocks) {
@@ -573,10 +654,40 @@ extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* fea
                            dense ? nullptr : aux + p->perm_offset, n, (hipStream_t)stream);
 }
 
+static int project_stage(prism_ctx* c, bool up, const prism_project_push* p, void* features, int32_t batch,
+                         void* stream) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
+    if (!p || !features) return fail(c, PRISM_ERR_INVALID, "push or features is NULL");
+    if (batch < 1 || p->n_tokens < 1) return fail(c, PRISM_ERR_INVALID, "batch %d / n_tokens %d < 1", batch, p->n_tokens);
+    const int64_t w = up ? c->aoffs.up_w : c->aoffs.down_w, b = up ? c->aoffs.up_b : c->aoffs.down_b;
+    if (p->w_offset != w || p->b_offset != b)
+        return fail(c, PRISM_ERR_INVALID, "projection weight offsets do not name the loaded %s adapter", up ? "up" : "down");
+    if (p->input_offset < 0 || p->output_offset < 0) return fail(c, PRISM_ERR_INVALID, "negative feature offset");
+    uint16_t* f = static_cast<uint16_t*>(features);
+    if (!aligned16(f + p->input_offset) || !aligned16(f + p->output_offset))
+        return fail(c, PRISM_ERR_INVALID, "feature offsets must be multiples of 8 elements");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return enqueue_project(c, up, f + p->input_offset, f + p->output_offset, (int64_t)batch * p->n_tokens,
+                           (hipStream_t)stream);
+}
+
+extern "C" int prism_project_up(prism_ctx* c, const prism_project_push* p, void* features, int32_t batch,
+                                void* stream) {
+    return project_stage(c, true, p, features, batch, stream);
+}
+
+extern "C" int prism_project_down(prism_ctx* c, const prism_project_push* p, void* features, int32_t batch,
+                                  void* stream) {
+    return project_stage(c, false, p, features, batch, stream);
+}
+
 /* ------------------------------------------------------------ block chain */
 
-static int ensure_workspace(prism_ctx* c, int batch) {
-    if (c->ws && c->ws_batch >= batch) return PRISM_OK;
+/* io: also the two chain-input/output buffers of the adapted chain */
+static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
+    if (c->ws && c->ws_batch >= batch && (!io || c->ws_io[0])) return PRISM_OK;
+    io = io || (c->ws && c->ws_io[0]); /* keep them once allocated */
     drop_graph(c);
     drop_workspace(c);
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
@@ -588,6 +699,8 @@ static int ensure_workspace(prism_ctx* c, int batch) {
     const size_t o_asg = ar.take((size_t)NB * n * 4);
     const size_t o_cnt = ar.take((size_t)NB * N * CHAIN_COUNT_STRIDE * 4);
     const size_t o_perm = ar.take((size_t)N * n * 4);
+    const size_t o_io0 = ar.take(io ? (size_t)n * D * 2 : 0);
+    const size_t o_io1 = ar.take(io ? (size_t)n * D * 2 : 0);
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, ar.off);
     if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for the workspace: %s", ar.off, hipGetErrorString(e));
@@ -605,6 +718,8 @@ static int ensure_workspace(prism_ctx* c, int batch) {
     c->ws_assign = reinterpret_cast<int32_t*>(b + o_asg);
     c->ws_counts = reinterpret_cast<int32_t*>(b + o_cnt);
     c->ws_perm = reinterpret_cast<int32_t*>(b + o_perm);
+    c->ws_io[0] = io ? reinterpret_cast<uint16_t*>(b + o_io0) : nullptr;
+    c->ws_io[1] = io ? reinterpret_cast<uint16_t*>(b + o_io1) : nullptr;
     c->counts_dirty = false; /* zero-filled above */
     return PRISM_OK;
 }
@@ -669,33 +784,47 @@ static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
     return PRISM_OK;
 }
 
-extern "C" int prism_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+/* The chain, optionally wrapped in the projection adapters: up(in ->
+ * ws_io[0]), blocks(ws_io[0] -> ws_io[1]), down(ws_io[1] -> out). */
+static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, bool adapted, hipStream_t s) {
+    if (!adapted) return enqueue_forward_impl(c, in, out, batch, s);
+    const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
+    int rc = enqueue_project(c, true, in, c->ws_io[0], n, s);
+    if (rc) return rc;
+    rc = enqueue_forward_impl(c, c->ws_io[0], c->ws_io[1], batch, s);
+    if (rc) return rc;
+    return enqueue_project(c, false, c->ws_io[1], out, n, s);
+}
+
+static int run_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
+    if (adapted && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
     HIP_TRY(c, hipSetDevice(c->device));
-    rc = ensure_workspace(c, batch);
+    rc = ensure_workspace(c, batch, adapted);
     if (rc) return rc;
     rc = clean_counts(c, (hipStream_t)stream);
     if (rc) return rc;
-    rc = enqueue_forward_impl(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
-                              (hipStream_t)stream);
+    rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, adapted,
+                       (hipStream_t)stream);
     if (rc) c->counts_dirty = true; /* launched part of the chain */
     return rc;
 }
 
-extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
+    if (adapted && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
     HIP_TRY(c, hipSetDevice(c->device));
-    if (!(c->gexec && c->g_in == in && c->g_out == out && c->g_batch == batch)) {
-        rc = ensure_workspace(c, batch);
+    if (!(c->gexec && c->g_in == in && c->g_out == out && c->g_batch == batch && c->g_adapted == adapted)) {
+        rc = ensure_workspace(c, batch, adapted);
         if (rc) return rc;
         drop_graph(c);
         HIP_TRY(c, hipStreamSynchronize(c->cap_stream));
         HIP_TRY(c, hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
         /* captured, not run: a failure here leaves the counters untouched */
-        rc = enqueue_forward_impl(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch,
-                                  c->cap_stream);
+        rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, adapted,
+                           c->cap_stream);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(c->cap_stream, &g);
         if (rc) {
@@ -712,11 +841,28 @@ extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int3
         c->g_in = in;
         c->g_out = out;
         c->g_batch = batch;
+        c->g_adapted = adapted;
     }
     rc = clean_counts(c, (hipStream_t)stream);
     if (rc) return rc;
     HIP_TRY(c, hipGraphLaunch(c->gexec, (hipStream_t)stream));
     return PRISM_OK;
+}
+
+extern "C" int prism_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    return run_forward(c, in, out, batch, stream, false);
+}
+
+extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    return run_forward_graph(c, in, out, batch, stream, false);
+}
+
+extern "C" int prism_forward_adapted(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    return run_forward(c, in, out, batch, stream, true);
+}
+
+extern "C" int prism_forward_adapted_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    return run_forward_graph(c, in, out, batch, stream, true);
 }
 
 extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_dev, int64_t* tokens_per_block) {

@@ -13,6 +13,8 @@ bool shape_supported(const prism_model_desc* d, std::string* why);
 int64_t layout_blocks(const prism_model_desc* d, prism_block_offsets* offs);
 int validate_blocks(const prism_model_desc* d, const prism_block_offsets* offs, int64_t total,
                     std::string* why);
+int validate_adapters(const prism_model_desc* d, const prism_adapter_offsets* a, int64_t total,
+                      std::string* why);
 void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst);
 float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);

@@ -138,6 +138,27 @@ int validate_blocks(const prism_model_desc* d, const prism_block_offsets* offs, 
     return PRISM_OK;
 }
 
+int validate_adapters(const prism_model_desc* d, const prism_adapter_offsets* a, int64_t total,
+                      std::string* why) {
+    if (!shape_supported(d, why)) return PRISM_ERR_UNSUPPORTED;
+    if (!a) { if (why) *why = "adapter offsets are NULL"; return PRISM_ERR_INVALID; }
+    if (a->in_dim != 128) {
+        if (why) *why = "adapter in_dim " + std::to_string(a->in_dim) + " (supported: 128)";
+        return PRISM_ERR_UNSUPPORTED;
+    }
+    const int64_t D = d->dim, I = a->in_dim;
+    struct { const char* name; int64_t off, n; } t[] = {
+        {"up_w", a->up_w, D * I}, {"up_b", a->up_b, D}, {"down_w", a->down_w, I * D}, {"down_b", a->down_b, I},
+    };
+    for (auto& x : t) {
+        if (!span_ok(x.off, x.n, total)) {
+            if (why) *why = std::string("adapter ") + x.name + " outside the blob or not 8-aligned";
+            return PRISM_ERR_BLOB;
+        }
+    }
+    return PRISM_OK;
+}
+
 void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst) {
     const int KS = K / 32;
     for (int rt = 0; rt < rows_padded / 16; ++rt)
@@ -212,6 +233,30 @@ extern "C" int prism_layout(const prism_model_desc* desc, prism_block_offsets* o
     }
     const int64_t n = layout_blocks(desc, offs);
     if (total) *total = n;
+    return PRISM_OK;
+}
+
+extern "C" int prism_adapter_layout(const prism_model_desc* desc, int32_t in_dim, int64_t base,
+                                    prism_adapter_offsets* offs, int64_t* end) {
+    std::string why;
+    if (!shape_supported(desc, &why)) {
+        set_global_error(why);
+        return PRISM_ERR_UNSUPPORTED;
+    }
+    if (in_dim != 128 || base < 0 || !offs) {
+        set_global_error("prism_adapter_layout: in_dim must be 128, base >= 0, offs non-NULL");
+        return PRISM_ERR_INVALID;
+    }
+    /* proj_up_w, proj_up_b, proj_dn_w, proj_dn_b (prism_moe_bench.cpp:351-352) */
+    int64_t cur = (base + 7) & ~int64_t(7);
+    const int64_t D = desc->dim;
+    offs->in_dim = in_dim;
+    offs->pad_ = 0;
+    offs->up_w = bump(cur, D * in_dim);
+    offs->up_b = bump(cur, D);
+    offs->down_w = bump(cur, (int64_t)in_dim * D);
+    offs->down_b = bump(cur, in_dim);
+    if (end) *end = cur;
     return PRISM_OK;
 }
 

@@ -79,4 +79,12 @@ typedef struct ExpertArgs {
     int32_t count_stride;
 } ExpertArgs;
 
+typedef struct ProjArgs {
+    const uint16_t* in;   /* [n_tokens][in_dim] fp16                      */
+    uint16_t* out;        /* [n_tokens][out_dim] fp16                     */
+    const uint16_t* w;    /* packed [out_dim/16][in_dim/32]               */
+    const float* b;       /* [out_dim]                                    */
+    int64_t n_tokens;
+} ProjArgs;
+
 #endif

@@ -21,7 +21,9 @@
  * registers) right behind the row loads, so W1 arrives while LN2 runs. GEMM1
  * refills the registers of its first KS/2 k-steps with the first half of W2
  * (in flight during GEMM1 and the GELU); GEMM2 issues the second half of W2
- * while it consumes the first.
+ * while it consumes the first. (Issuing all of W2 up front, which the 8-wave
+ * variant has the registers for, was measured slower: the rows and W1 then
+ * retire behind it.)
  *
  * GEMMs are C^T = W * A^T (weights as the A operand, tokens as columns), so a
  * lane's accumulator holds 4 consecutive channels of one token: 8-byte LDS

@@ -7,11 +7,13 @@
  *   prism_attn_d{256,128}[_w8]_r{1..4}             attention + fused routing
  *   prism_router_d{256,128}_n{1..4}                router + counting sort
  *   prism_expert_d{256,128}_bm64                   grouped expert FFN
+ *   prism_project_{up,down}_d{256,128}             projection adapters (128 <-> dim)
  *   prism_zero_i32                                 clears routing counters
  */
 #include "attn.hpp"
 #include "router.hpp"
 #include "expert.hpp"
+#include "project.hpp"
 
 /* Routing counters must start at zero; a kernel (not a memset node) keeps
  * the launch safe under stream capture. */

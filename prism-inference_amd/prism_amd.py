@@ -83,6 +83,16 @@ class ExpertPush(C.Structure):
                 ("perm_offset", C.c_int64)]
 
 
+class AdapterOffsets(C.Structure):
+    _fields_ = [("in_dim", C.c_int32), ("pad_", C.c_int32), ("up_w", C.c_int64), ("up_b", C.c_int64),
+                ("down_w", C.c_int64), ("down_b", C.c_int64)]
+
+
+class ProjectPush(C.Structure):
+    _fields_ = [("n_tokens", C.c_int32), ("pad_", C.c_int32), ("w_offset", C.c_int64),
+                ("b_offset", C.c_int64), ("input_offset", C.c_int64), ("output_offset", C.c_int64)]
+
+
 # Every entry point the header declares: name -> (restype, argtypes)
 _P = C.c_void_p
 SIGNATURES = {
@@ -105,6 +115,13 @@ SIGNATURES = {
     "prism_forward_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
     "prism_forward_assignments": (C.c_int, [_P, C.POINTER(_P), C.POINTER(C.c_int64)]),
     "prism_aux_elems": (C.c_int64, [C.c_int32, C.c_int64]),
+    "prism_adapter_layout": (C.c_int, [C.POINTER(ModelDesc), C.c_int32, C.c_int64, C.POINTER(AdapterOffsets),
+                                       C.POINTER(C.c_int64)]),
+    "prism_load_adapters": (C.c_int, [_P, _P, C.c_size_t, C.POINTER(AdapterOffsets)]),
+    "prism_project_up": (C.c_int, [_P, C.POINTER(ProjectPush), _P, C.c_int32, _P]),
+    "prism_project_down": (C.c_int, [_P, C.POINTER(ProjectPush), _P, C.c_int32, _P]),
+    "prism_forward_adapted": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_forward_adapted_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
 }
 
 _lib = None
@@ -220,6 +237,28 @@ def synth_features(cfg: Config, batch: int | None = None, seed: int = 0, H=None,
     h = cfg.H if H is None else H
     w = cfg.W if W is None else W
     return synth_normal(b * h * w * cfg.dim, seed=seed, stream=0, std=1.0).reshape(b, h * w, cfg.dim)
+
+
+ADAPTER_IN = 128  # encoder channels either side of the block chain
+
+
+def adapter_layout(desc: ModelDesc, base: int = 0, in_dim: int = ADAPTER_IN):
+    """(AdapterOffsets, end element) for the adapters placed from `base` on."""
+    a = AdapterOffsets()
+    end = C.c_int64()
+    _check(lib().prism_adapter_layout(C.byref(desc), in_dim, base, C.byref(a), C.byref(end)))
+    return a, end.value
+
+
+def synth_adapters(desc: ModelDesc, seed: int = 0, in_dim: int = ADAPTER_IN, std: float = 0.02):
+    """(blob uint16, AdapterOffsets): both projections ~N(0, std^2), weights
+    and biases alike, from the same generator as the blocks (own streams)."""
+    a, end = adapter_layout(desc, 0, in_dim)
+    blob = np.zeros(end, dtype=np.uint16)
+    D = desc.dim
+    for k, (off, n) in enumerate(((a.up_w, D * in_dim), (a.up_b, D), (a.down_w, in_dim * D), (a.down_b, in_dim))):
+        blob[off:off + n] = synth_normal(n, seed=seed, stream=(0xAD << 24) | k, std=std)
+    return blob, a
 
 
 def pack_weight(w: np.ndarray, rows_padded: int | None = None) -> np.ndarray:
@@ -375,9 +414,26 @@ class Engine:
                 stream: int | None = None) -> int:
         return self.L.prism_experts(self.h, C.byref(push), features, aux, batch, stream)
 
-    def forward(self, x: int, y: int, batch: int, stream: int | None = None, graph: bool = False):
-        f = self.L.prism_forward_graph if graph else self.L.prism_forward
+    def forward(self, x: int, y: int, batch: int, stream: int | None = None, graph: bool = False,
+                adapted: bool = False):
+        if adapted:
+            f = self.L.prism_forward_adapted_graph if graph else self.L.prism_forward_adapted
+        else:
+            f = self.L.prism_forward_graph if graph else self.L.prism_forward
         _check(f(self.h, x, y, batch, stream), self.h)
+
+    def load_adapters(self, blob: np.ndarray, aoffs: AdapterOffsets):
+        blob = np.ascontiguousarray(blob, dtype=np.uint16)
+        _check(self.L.prism_load_adapters(self.h, _ptr(blob), blob.nbytes, C.byref(aoffs)), self.h)
+        self.aoffs = aoffs
+
+    def project(self, up: bool, push: ProjectPush, features: int, batch: int, stream: int | None = None) -> int:
+        f = self.L.prism_project_up if up else self.L.prism_project_down
+        return f(self.h, C.byref(push), features, batch, stream)
+
+    def project_push(self, up: bool, n_tokens: int, in_off: int, out_off: int) -> ProjectPush:
+        a = self.aoffs
+        return ProjectPush(n_tokens, 0, a.up_w if up else a.down_w, a.up_b if up else a.down_b, in_off, out_off)
 
     def forward_assignments(self):
         p = C.c_void_p()

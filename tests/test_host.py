@@ -208,7 +208,34 @@ def test_context_calls_fail_cleanly_without_a_context():
     assert L.prism_attn(None, C.byref(push), None, 1, None) == P.ERR_INVALID
     assert L.prism_forward(None, None, None, 1, None) == P.ERR_INVALID
     assert L.prism_load_weights(None, None, None, 0, None) == P.ERR_INVALID
+    assert L.prism_load_adapters(None, None, 0, None) == P.ERR_INVALID
+    assert L.prism_project_up(None, C.byref(P.ProjectPush()), None, 1, None) == P.ERR_INVALID
+    assert L.prism_project_down(None, C.byref(P.ProjectPush()), None, 1, None) == P.ERR_INVALID
+    assert L.prism_forward_adapted(None, None, None, 1, None) == P.ERR_INVALID
+    assert L.prism_forward_adapted_graph(None, None, None, 1, None) == P.ERR_INVALID
     L.prism_destroy(None)  # no-op
+
+
+@pytest.mark.parametrize("name", ["moe64", "dense128"])
+def test_adapter_layout(name):
+    """The adapters follow the reference's wa() order (proj_up_w, proj_up_b,
+    proj_dn_w, proj_dn_b), 8-aligned, from an arbitrary base."""
+    cfg = P.CONFIGS[name]
+    desc = cfg.desc(n_blocks=1)
+    _, total = P.layout(desc)
+    a, end = P.adapter_layout(desc, total + 3)
+    D, I = cfg.dim, 128
+    assert a.in_dim == I and a.up_w == (total + 3 + 7) // 8 * 8
+    assert a.up_b == a.up_w + D * I and a.down_w == a.up_b + (D + 7) // 8 * 8
+    assert a.down_b == a.down_w + I * D and end == a.down_b + I
+    assert all(v % 8 == 0 for v in (a.up_w, a.up_b, a.down_w, a.down_b))
+    with pytest.raises(P.PrismError):
+        P.adapter_layout(desc, 0, in_dim=64)
+    blob, a2 = P.synth_adapters(desc, seed=1)
+    blob2, _ = P.synth_adapters(desc, seed=1)
+    assert a2.up_w == 0 and (blob == blob2).all() and blob.size == end - a.up_w  # same span from base 0
+    w = blob[a2.up_w:a2.up_w + D * I].view(np.float16).astype(np.float32)
+    assert abs(w.std() - 0.02) < 0.002
 
 
 def test_create_reports_missing_code_object():

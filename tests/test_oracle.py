@@ -329,3 +329,49 @@ def test_stage_rejects_bad_config():
     with pytest.raises(ValueError):
         O.expert_stage(O.cfg(256, 8, 32, 16, 12, 20, 1), w, offs[0], feats(cfg, 12, 20, 1),
                        np.full(240, 16, np.int32))   # expert id out of range
+
+
+# ------------------------------------------------------------------ projection adapters
+
+def _f16(x):
+    return x.astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("in_dim,out_dim,relu", [(128, 256, True), (256, 128, False), (128, 128, True)])
+def test_project_matches_torch_linear(in_dim, out_dim, relu):
+    """fp32 mode against torch's linear (+ relu) in fp64; faithful mode is the
+    fp32 value rounded to fp16 once (coopVecMatMulAddNV's fp16 result)."""
+    rng = np.random.default_rng(in_dim + out_dim)
+    x = _f16(rng.standard_normal((300, in_dim)))
+    W = _f16(rng.standard_normal((out_dim, in_dim)) * 0.05)
+    b = _f16(rng.standard_normal(out_dim) * 0.05)
+    ref = F.linear(torch.tensor(x, dtype=torch.float64), torch.tensor(W, dtype=torch.float64),
+                   torch.tensor(b, dtype=torch.float64))
+    if relu:
+        ref = F.relu(ref)
+    ref = ref.numpy()
+    got32 = O.project(W, b, x, relu, faithful=False)
+    assert np.abs(got32 - ref).max() < 1e-5
+    got16 = O.project(W, b, x, relu, faithful=True)
+    assert (got16 == _f16(got32)).all()
+    if relu:
+        assert (got16 >= 0).all() and (got16 == 0).mean() > 0.3
+
+
+def test_project_closed_forms():
+    """[I; -I] with ReLU gives [relu(x); relu(-x)]; [I, I] gives the fp16 of
+    x[:128] + x[128:] (exact sums of fp16 values, rounded once); zero weights
+    give the bias."""
+    rng = np.random.default_rng(7)
+    x = _f16(rng.standard_normal((64, 128)))
+    up = np.vstack([np.eye(128), -np.eye(128)]).astype(np.float32)
+    y = O.project(up, np.zeros(256, np.float32), x, True)
+    assert (y == np.hstack([np.maximum(x, 0), np.maximum(-x, 0)])).all()
+    x2 = _f16(rng.standard_normal((64, 256)))
+    dn = np.hstack([np.eye(128), np.eye(128)]).astype(np.float32)
+    y2 = O.project(dn, np.zeros(128, np.float32), x2, False)
+    exact = x2[:, :128].astype(np.float64) + x2[:, 128:]
+    assert (y2 == exact.astype(np.float16).astype(np.float32)).all()
+    bias = _f16(rng.standard_normal(256))
+    y3 = O.project(np.zeros((256, 128), np.float32), bias, x, True)
+    assert (y3 == np.maximum(bias, 0)[None, :]).all()
