@@ -38,15 +38,15 @@ def attn_flops_per_token(cfg):
     return 2 * (3 * d * d + 2 * 64 * d + d * d)
 
 
-def time_graph(hip, eng, dx, dy, batch, steps, warmup, stream):
+def time_graph(hip, eng, dx, dy, batch, steps, warmup, stream, adapted=False):
     for _ in range(warmup):
-        eng.forward(dx, dy, batch, stream, graph=True)
+        eng.forward(dx, dy, batch, stream, graph=True, adapted=adapted)
     hip.sync()
     e0, e1 = hip.event(), hip.event()
     t0 = time.perf_counter()
     hip.record(e0, stream)
     for _ in range(steps):
-        eng.forward(dx, dy, batch, stream, graph=True)
+        eng.forward(dx, dy, batch, stream, graph=True, adapted=adapted)
     hip.record(e1, stream)
     ms = hip.elapsed_ms(e0, e1)
     hip.sync()
@@ -176,6 +176,30 @@ def main():
     attn_grid = ((cfg.W + 7) // 8) * ((cfg.H + 7) // 8) * B
     traffic, traffic_src = measured_traffic("prism_attn_d256", attn_grid) if cfg.name == "moe64" else (None, None)
 
+    # ---- projection adapters (next to the chain): per launch at batch B, and the
+    # adapted chain (up -> blocks -> down) as one graph step
+    ablob, aoffs = P.synth_adapters(desc, seed=0)
+    eng.load_adapters(ablob, aoffs)
+    I = aoffs.in_dim
+    proj = hip.malloc(n * (I + d) * 2)
+    hip.upload(proj, P.synth_normal(n * I, seed=2))
+    up_push = eng.project_push(True, T, 0, n * I)
+    dn_push = eng.project_push(False, T, n * I, 0)
+    t_up = time_stage(hip, lambda: eng.project(True, up_push, proj, B, stream), args.stage_reps, stream)
+    t_dn = time_stage(hip, lambda: eng.project(False, dn_push, proj, B, stream), args.stage_reps, stream)
+    ax, ay = hip.malloc(n * I * 2), hip.malloc(n * I * 2)
+    hip.copy(ax, proj, n * I * 2)
+    ms_ad, _ = time_graph(hip, eng, ax, ay, B, max(5, args.steps // 2), 2, stream, adapted=True)
+    proj_bytes = n * (I + d) * 2 + (I * d * 2 + (I + d) * 4)  # activations in + out, weights + biases once
+    adapters = {"up_ms": round(t_up, 5), "down_ms": round(t_dn, 5),
+                "up_hbm_frac": round(proj_bytes / (t_up * 1e-3) / HBM_PEAK, 4),
+                "down_hbm_frac": round(proj_bytes / (t_dn * 1e-3) / HBM_PEAK, 4),
+                "bytes_per_launch": proj_bytes,
+                "adapted_chain_ms_per_step": round(ms_ad, 5),
+                "note": "pw_project 128->256 (+ReLU) and 256->128 around the 16 blocks, batch " + str(B)}
+    for ptr in (proj, ax, ay):
+        hip.free(ptr)
+
     # ---- expert load actually produced (all blocks, batch B)
     share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
     hist0 = np.bincount(assign[0], minlength=N)
@@ -214,6 +238,7 @@ def main():
                         "hottest_share_mean": round(float(share.mean()), 4),
                         "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},
         "wall_s_timed": round(wall_b, 3),
+        "adapters": adapters,
     }
     hip.free(feats)
     hip.free(aux)
