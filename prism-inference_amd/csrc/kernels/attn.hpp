@@ -244,8 +244,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kt][i]);
-            m = fmaxf(m, __shfl_xor(m, 16, 64));
-            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            m = max_groups(m);
             /* exp(scale * (s - m)) = 2^(s * sl2 - m * sl2) */
             const float msl = m * sl2;
             float sum = 0.f;
@@ -259,8 +258,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                 }
                 p[kt][qt] = cvt_h4(e);
             }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
+            sum = sum_groups(sum);
             inv[qt] = fast_rcp(fmaxf(sum, 1e-6f));
         }
 

@@ -38,11 +38,65 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-/* Sum over groups of `width` consecutive lanes (width a power of two <= 64). */
+/*
+ * Cross-lane reductions without the LDS crossbar (ds_bpermute, ~100 cycles
+ * each): gfx950's v_permlane16_swap / v_permlane32_swap with both operands x
+ * return (x of lane l & ~16, x of lane l | 16) (resp. 32), so op(r0, r1) is
+ * x op x[l ^ 16] in every lane, and DPP row permutations combine lanes
+ * within a row of 16. Every pairing is symmetric (both lanes of a pair
+ * compute the same a op b), so all lanes of a group end with identical bits.
+ */
+__device__ __forceinline__ void lanes_x16(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    a = __builtin_bit_cast(float, (unsigned)r[0]);
+    b = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ void lanes_x32(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    a = __builtin_bit_cast(float, (unsigned)r[0]);
+    b = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ void lanes_x16(int v, int& a, int& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    a = (int)r[0];
+    b = (int)r[1];
+}
+__device__ __forceinline__ void lanes_x32(int v, int& a, int& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    a = (int)r[0];
+    b = (int)r[1];
+}
+/* v + v[l ^ 16] + v[l ^ 32] + v[l ^ 48]: sum over the 4 lane groups */
+__device__ __forceinline__ float sum_groups(float v) {
+    float a, b;
+    lanes_x16(v, a, b);
+    lanes_x32(a + b, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float max_groups(float v) {
+    float a, b;
+    lanes_x16(v, a, b);
+    lanes_x32(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+/* Sum over groups of WIDTH (4, 8 or 16) consecutive lanes, on DPP:
+ * quad_perm xor 1, quad_perm xor 2, then row_half_mirror (pairs the two
+ * quads of each 8-lane half) and, for 16, row_mirror first (pairs quad q
+ * with quad 3 - q). */
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = 1; m < WIDTH; m <<= 1) v += __shfl_xor(v, m, 64);
+    static_assert(WIDTH == 4 || WIDTH == 8 || WIDTH == 16, "group width");
+    v += dpp<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v += dpp<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    if constexpr (WIDTH == 16) v += dpp<0x140>(v); /* row_mirror      */
+    if constexpr (WIDTH >= 8) v += dpp<0x141>(v);  /* row_half_mirror */
     return v;
 }
 

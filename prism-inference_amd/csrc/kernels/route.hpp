@@ -29,8 +29,7 @@ __device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float*
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int j = 0; j < 8; ++j) s += (float)cur[ks][j];
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
+    s = sum_groups(s);
     const float mean = s * (1.0f / DIM);
     float q = 0.f;
 #pragma unroll
@@ -40,8 +39,7 @@ __device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float*
             const float t = (float)cur[ks][j] - mean;
             q = __builtin_fmaf(t, t, q);
         }
-    q += __shfl_xor(q, 16, 64);
-    q += __shfl_xor(q, 32, 64);
+    q = sum_groups(q);
     const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -74,13 +72,23 @@ __device__ __forceinline__ void route_tile_best(const f4& acc, int rt, int g, fl
     }
 }
 
+/* (a_v, a_e) vs (b_v, b_e): larger logit, then lower id. Symmetric, so the
+ * two lanes of a pair agree. */
+__device__ __forceinline__ void route_pick(float av, int ae, float bv, int be, float& v, int& e) {
+    const bool b_wins = bv > av || (bv == av && be < ae);
+    v = b_wins ? bv : av;
+    e = b_wins ? be : ae;
+}
+
 __device__ __forceinline__ void route_combine_groups(float& best_v, int& best_e) {
-#pragma unroll
-    for (int m = 16; m <= 32; m <<= 1) {
-        const float ov = __shfl_xor(best_v, m, 64);
-        const int oe = __shfl_xor(best_e, m, 64);
-        if (ov > best_v || (ov == best_v && oe < best_e)) { best_v = ov; best_e = oe; }
-    }
+    float av, bv;
+    int ae, be;
+    lanes_x16(best_v, av, bv);
+    lanes_x16(best_e, ae, be);
+    route_pick(av, ae, bv, be, best_v, best_e);
+    lanes_x32(best_v, av, bv);
+    lanes_x32(best_e, ae, be);
+    route_pick(av, ae, bv, be, best_v, best_e);
 }
 
 /* frag(rt, ks) returns router fragment (row tile rt, k-step ks) of the packed
