@@ -19,6 +19,7 @@ typedef _Float16 f16;
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 #define PRISM_LN_EPS 1e-5f
 
@@ -168,6 +169,31 @@ __device__ __forceinline__ h4 cvt_h4(f4 v) {
  * variance in fp32; output rounded to fp16; invalid rows are written as
  * zeros. g and b live in LDS.
  */
+/* LayerNorm building blocks (biased variance, eps 1e-5, fp32 statistics):
+ * the sum and the sum of squares of fp16 values come straight from the fp16
+ * pairs on v_dot2_f32_f16 (products exact, fp32 accumulation), the variance
+ * is E[x^2] - mean^2 (clamped at 0), and each value is normalised as
+ * z = fma(x, inv, -mean*inv) with the fp16 x as a mixed-precision operand,
+ * then y = fma(z, gamma, beta). */
+__device__ __forceinline__ void moments8(const h8& x, float& s, float& q) {
+    const h2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const h2 p = {x[j], x[j + 1]};
+        s = __builtin_amdgcn_fdot2(p, one, s, false);
+        q = __builtin_amdgcn_fdot2(p, p, q, false);
+    }
+}
+template <int N>
+__device__ __forceinline__ float ln_inv(float s, float q, float& mean) {
+    mean = s * (1.0f / N);
+    const float var = fmaxf(__builtin_fmaf(-mean, mean, q * (1.0f / N)), 0.f);
+    return __builtin_amdgcn_rsqf(var + PRISM_LN_EPS); /* v_rsq_f32, 1 ulp; argument >= 1e-5 */
+}
+__device__ __forceinline__ float ln_apply(f16 x, float inv, float nmi, float g, float b) {
+    return __builtin_fmaf(__builtin_fmaf((float)x, inv, nmi), g, b);
+}
+
 struct RowChunk {
     h8 a0, a1;
 };
@@ -195,33 +221,25 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const f
         rd[0] = rc.a0;
         rd[1] = rc.a1;
     }
-    float v[16];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { v[j] = (float)rc.a0[j]; v[8 + j] = (float)rc.a1[j]; }
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s += v[j];
+    float s = 0.f, q = 0.f;
+    moments8(rc.a0, s, q);
+    moments8(rc.a1, s, q);
     s = group_sum<LPS>(s);
-    const float mean = s * (1.0f / DIM);
-    float q = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        v[j] -= mean;
-        q = __builtin_fmaf(v[j], v[j], q);
-    }
     q = group_sum<LPS>(q);
-    const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
+    float mean;
+    const float inv = ln_inv<DIM>(s, q, mean);
+    const float nmi = -mean * inv;
     h8 o0, o1;
 #pragma unroll
     for (int j = 0; j < 8; j += 4) {
-        const f4 n0 = {__builtin_fmaf(v[j], inv * g[c0 + j], b[c0 + j]),
-                       __builtin_fmaf(v[j + 1], inv * g[c0 + j + 1], b[c0 + j + 1]),
-                       __builtin_fmaf(v[j + 2], inv * g[c0 + j + 2], b[c0 + j + 2]),
-                       __builtin_fmaf(v[j + 3], inv * g[c0 + j + 3], b[c0 + j + 3])};
-        const f4 n1 = {__builtin_fmaf(v[8 + j], inv * g[c0 + 8 + j], b[c0 + 8 + j]),
-                       __builtin_fmaf(v[9 + j], inv * g[c0 + 9 + j], b[c0 + 9 + j]),
-                       __builtin_fmaf(v[10 + j], inv * g[c0 + 10 + j], b[c0 + 10 + j]),
-                       __builtin_fmaf(v[11 + j], inv * g[c0 + 11 + j], b[c0 + 11 + j])};
+        const f4 n0 = {ln_apply(rc.a0[j], inv, nmi, g[c0 + j], b[c0 + j]),
+                       ln_apply(rc.a0[j + 1], inv, nmi, g[c0 + j + 1], b[c0 + j + 1]),
+                       ln_apply(rc.a0[j + 2], inv, nmi, g[c0 + j + 2], b[c0 + j + 2]),
+                       ln_apply(rc.a0[j + 3], inv, nmi, g[c0 + j + 3], b[c0 + j + 3])};
+        const f4 n1 = {ln_apply(rc.a1[j], inv, nmi, g[c0 + 8 + j], b[c0 + 8 + j]),
+                       ln_apply(rc.a1[j + 1], inv, nmi, g[c0 + 9 + j], b[c0 + 9 + j]),
+                       ln_apply(rc.a1[j + 2], inv, nmi, g[c0 + 10 + j], b[c0 + 10 + j]),
+                       ln_apply(rc.a1[j + 3], inv, nmi, g[c0 + 11 + j], b[c0 + 11 + j])};
         const h4 p0 = cvt_h4(n0), p1 = cvt_h4(n1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

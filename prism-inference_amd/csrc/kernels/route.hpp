@@ -24,23 +24,14 @@ template <int DIM>
 __device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b, int g,
                                          h8 (&hn)[DIM / 32]) {
     constexpr int KS = DIM / 32;
-    float s = 0.f;
+    float s = 0.f, q = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s += (float)cur[ks][j];
+    for (int ks = 0; ks < KS; ++ks) moments8(cur[ks], s, q);
     s = sum_groups(s);
-    const float mean = s * (1.0f / DIM);
-    float q = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float t = (float)cur[ks][j] - mean;
-            q = __builtin_fmaf(t, t, q);
-        }
     q = sum_groups(q);
-    const float inv = 1.0f / sqrtf(q * (1.0f / DIM) + PRISM_LN_EPS);
+    float mean;
+    const float inv = ln_inv<DIM>(s, q, mean);
+    const float nmi = -mean * inv;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         asm volatile("" ::: "memory"); /* keep this k-step's gamma/beta reads here */
@@ -50,7 +41,7 @@ __device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float*
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int c = 32 * ks + 8 * g + j + i;
-                t[i] = __builtin_fmaf((float)cur[ks][j + i] - mean, inv * s_g[c], s_b[c]);
+                t[i] = ln_apply(cur[ks][j + i], inv, nmi, s_g[c], s_b[c]);
             }
             const h4 q4 = cvt_h4(t);
 #pragma unroll
