@@ -185,12 +185,18 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             for (int t = 0; t < 4; ++t) { accQ[c][t] = bq; accK[c][t] = bk; accV[t][c] = f4{bv, bv, bv, bv}; }
         }
 
+        /* B operands double-buffered: k-step ks+1's LDS reads go out before
+         * k-step ks's MFMAs, so their latency hides behind them */
+        h8 xf[4], xn[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            h8 xf[4];
+            if (ks + 1 < KS) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-                xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+                for (int t = 0; t < 4; ++t)
+                    xn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+            }
 #pragma unroll
             for (int f = 0; f < S::FPK; ++f) {
                 const int p = hh * S::HEADF + ks * S::FPK + f;
@@ -204,6 +210,10 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                 }
                 if (p + PF < S::TOTAL && p + PF < total)
                     ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
+            }
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xf[t] = xn[t];
             }
             sched_fence();
         }
@@ -319,12 +329,16 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[r][t] = bo;
     }
+    h8 of[4], on[4]; /* double-buffered like the QKV operands */
+#pragma unroll
+    for (int t = 0; t < 4; ++t) of[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        h8 of[4];
+        if (ks + 1 < KS) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-            of[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+            for (int t = 0; t < 4; ++t)
+                on[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+        }
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
             const int p = S::HPW * S::HEADF + ks * ORT + r;
@@ -333,6 +347,10 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             for (int t = 0; t < 4; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
             if (p + PF < S::TOTAL && p + PF < total)
                 ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
+        }
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) of[t] = on[t];
         }
         sched_fence();
     }

@@ -147,17 +147,25 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             for (int t = 0; t < TT; ++t) acc[r][t] = bb;
         }
         /* GEMM1: hidden rows [wave*RT*16, +RT*16) for all BM tokens */
+        h8 xf[TT], xn[TT]; /* k-step ks+1's operands load during ks's MFMAs */
+#pragma unroll
+        for (int t = 0; t < TT; ++t) xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            h8 xf[TT];
+            if (ks + 1 < KS) {
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
-                xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+                for (int t = 0; t < TT; ++t)
+                    xn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+            }
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
 #pragma unroll
                 for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
                 if (ks < KS / 2) wf[r][ks] = w2.load((wave * RT + r) * KS + ks, loff);
+            }
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TT; ++t) xf[t] = xn[t];
             }
             sched_fence();
         }
@@ -179,17 +187,24 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         __syncthreads();
         /* GEMM2 */
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            h8 xf[TT];
+        for (int t = 0; t < TT; ++t) xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
-                xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+                    xn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+            }
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
 #pragma unroll
                 for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
                 /* second half of W2, issued one half ahead of its use */
                 if (ks < KS / 2) wf[r][ks + KS / 2] = w2.load((wave * RT + r) * KS + ks + KS / 2, loff);
+            }
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TT; ++t) xf[t] = xn[t];
             }
             sched_fence();
         }
