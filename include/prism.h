@@ -183,6 +183,18 @@ int prism_router(prism_ctx* ctx, const prism_router_push* p, const void* feature
 int prism_experts(prism_ctx* ctx, const prism_expert_push* p, void* features,
                   int32_t* aux, int32_t batch, void* stream);
 
+/* Attention and router stages in ONE launch: the attention kernel routes its
+ * output tile before storing it (LN2 + router GEMM + argmax + counting sort
+ * in its epilogue), replacing the two dispatches
+ * prism_moe_bench.cpp:266-275. pr must name the same block as pa and read
+ * its output (pr->input_offset == pa->output_offset, same n_tokens); the
+ * features at pa->output_offset, assignment, counts and perm come out as
+ * prism_attn followed by prism_router would leave them (bit-identical expert
+ * ids and counts; the order inside a bucket is unspecified). No reference
+ * counterpart as a single call: the block chain uses it for MoE blocks. */
+int prism_attn_route(prism_ctx* ctx, const prism_attn_push* pa, const prism_router_push* pr,
+                     void* features, int32_t* aux, int32_t batch, void* stream);
+
 /* ---- whole block chain -------------------------------------------------- */
 
 /* Run all loaded blocks on `batch` frames: in and out are device fp16

@@ -575,7 +575,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-extern "C" int prism_attn(prism_ctx* c, const prism_attn_push* p, void* features, int32_t batch, void* stream) {
+static int check_attn(prism_ctx* c, const prism_attn_push* p, void* features, int32_t batch, const DevBlock** kb) {
     if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
     if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
     if (!p || !features) return fail(c, PRISM_ERR_INVALID, "push or features is NULL");
@@ -596,13 +596,12 @@ extern "C" int prism_attn(prism_ctx* c, const prism_attn_push* p, void* features
     uint16_t* f = static_cast<uint16_t*>(features);
     if (!aligned16(f + p->input_offset) || !aligned16(f + p->output_offset))
         return fail(c, PRISM_ERR_INVALID, "feature offsets must be 16-byte aligned (multiples of 8 elements)");
-    HIP_TRY(c, hipSetDevice(c->device));
-    return enqueue_attn(c, *k, f + p->input_offset, f + p->output_offset, p->spatial_h, p->spatial_w, batch,
-                        (hipStream_t)stream);
+    *kb = k;
+    return PRISM_OK;
 }
 
-extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void* features, int32_t* aux,
-                            int32_t batch, void* stream) {
+static int check_router(prism_ctx* c, const prism_router_push* p, const void* features, int32_t* aux, int32_t batch,
+                        const DevBlock** kb) {
     if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
     if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
     if (!p || !features || !aux) return fail(c, PRISM_ERR_INVALID, "push, features or aux is NULL");
@@ -619,11 +618,51 @@ extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void
         return fail(c, PRISM_ERR_INVALID, "negative offset");
     const uint16_t* f = static_cast<const uint16_t*>(features);
     if (!aligned16(f + p->input_offset)) return fail(c, PRISM_ERR_INVALID, "input_offset must be a multiple of 8");
-    HIP_TRY(c, hipSetDevice(c->device));
-    const int rc = enqueue_zero(c, aux + p->count_offset, p->n_experts, (hipStream_t)stream);
+    *kb = k;
+    return PRISM_OK;
+}
+
+extern "C" int prism_attn(prism_ctx* c, const prism_attn_push* p, void* features, int32_t batch, void* stream) {
+    const DevBlock* k = nullptr;
+    const int rc = check_attn(c, p, features, batch, &k);
     if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    uint16_t* f = static_cast<uint16_t*>(features);
+    return enqueue_attn(c, *k, f + p->input_offset, f + p->output_offset, p->spatial_h, p->spatial_w, batch,
+                        (hipStream_t)stream);
+}
+
+extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void* features, int32_t* aux,
+                            int32_t batch, void* stream) {
+    const DevBlock* k = nullptr;
+    int rc = check_router(c, p, features, aux, batch, &k);
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    rc = enqueue_zero(c, aux + p->count_offset, p->n_experts, (hipStream_t)stream);
+    if (rc) return rc;
+    const uint16_t* f = static_cast<const uint16_t*>(features);
     return enqueue_router(c, *k, f + p->input_offset, aux + p->assignment_offset, aux + p->count_offset,
-                          aux + p->perm_offset, n, (hipStream_t)stream);
+                          aux + p->perm_offset, (int64_t)batch * p->n_tokens, (hipStream_t)stream);
+}
+
+extern "C" int prism_attn_route(prism_ctx* c, const prism_attn_push* pa, const prism_router_push* pr, void* features,
+                                int32_t* aux, int32_t batch, void* stream) {
+    const DevBlock *ka = nullptr, *kr = nullptr;
+    int rc = check_attn(c, pa, features, batch, &ka);
+    if (rc) return rc;
+    rc = check_router(c, pr, features, aux, batch, &kr);
+    if (rc) return rc;
+    if (ka != kr) return fail(c, PRISM_ERR_INVALID, "attention and router pushes name different blocks");
+    if (pr->input_offset != pa->output_offset || pr->n_tokens != pa->n_tokens)
+        return fail(c, PRISM_ERR_INVALID, "the router must read the attention output (input_offset %lld != %lld)",
+                    (long long)pr->input_offset, (long long)pa->output_offset);
+    HIP_TRY(c, hipSetDevice(c->device));
+    rc = enqueue_zero(c, aux + pr->count_offset, pr->n_experts, (hipStream_t)stream);
+    if (rc) return rc;
+    uint16_t* f = static_cast<uint16_t*>(features);
+    const RouteOut ro{aux + pr->assignment_offset, aux + pr->count_offset, aux + pr->perm_offset, 1, nullptr};
+    return enqueue_attn(c, *ka, f + pa->input_offset, f + pa->output_offset, pa->spatial_h, pa->spatial_w, batch,
+                        (hipStream_t)stream, &ro);
 }
 
 extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* features, int32_t* aux, int32_t batch,

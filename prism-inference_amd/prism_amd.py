@@ -109,6 +109,7 @@ SIGNATURES = {
     "prism_load_weights": (C.c_int, [_P, C.POINTER(ModelDesc), _P, C.c_size_t, C.POINTER(BlockOffsets)]),
     "prism_load_weights_file": (C.c_int, [_P, C.POINTER(ModelDesc), C.c_char_p, C.POINTER(BlockOffsets)]),
     "prism_attn": (C.c_int, [_P, C.POINTER(AttnPush), _P, C.c_int32, _P]),
+    "prism_attn_route": (C.c_int, [_P, C.POINTER(AttnPush), C.POINTER(RouterPush), _P, _P, C.c_int32, _P]),
     "prism_router": (C.c_int, [_P, C.POINTER(RouterPush), _P, _P, C.c_int32, _P]),
     "prism_experts": (C.c_int, [_P, C.POINTER(ExpertPush), _P, _P, C.c_int32, _P]),
     "prism_forward": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
@@ -406,6 +407,10 @@ class Engine:
 
     def attn(self, push: AttnPush, features: int, batch: int, stream: int | None = None) -> int:
         return self.L.prism_attn(self.h, C.byref(push), features, batch, stream)
+
+    def attn_route(self, pa: AttnPush, pr: RouterPush, features: int, aux: int, batch: int,
+                   stream: int | None = None) -> int:
+        return self.L.prism_attn_route(self.h, C.byref(pa), C.byref(pr), features, aux, batch, stream)
 
     def router(self, push: RouterPush, features: int, aux: int, batch: int, stream: int | None = None) -> int:
         return self.L.prism_router(self.h, C.byref(push), features, aux, batch, stream)

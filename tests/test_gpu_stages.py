@@ -162,3 +162,68 @@ def test_dense_ffn_stage(hip, engine, device_arena, name, H, W, batch):
     mx, mean = errors(f16(y).reshape(n, d), ref)
     print(f"[dense] {name}: max {mx:.3g} mean {mean:.3g}")
     assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
+FUSED_EXTRA = {
+    "moe40": P.Config("moe40", 256, 2, 8, 32, 40, 68, 120, 1, P.ROUTE_UNIFORM),
+    "moe24d128": P.Config("moe24d128", 128, 2, 8, 16, 24, 68, 120, 1, P.ROUTE_ZIPF),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,H,W,batch", [
+    ("moe64", 68, 120, 1),      # 8-wave kernel
+    ("moe64", 68, 120, 4),      # 4-wave kernel
+    ("moe16", 9, 13, 1),        # one row tile, ragged windows
+    ("moe40", 68, 120, 1),      # 3 row tiles, 24 padded experts
+    ("moe24d128", 68, 120, 2),
+])
+def test_attn_route_equals_attn_then_router(hip, engine, device_arena, name, H, W, batch):
+    """The fused launch leaves exactly what prism_attn + prism_router leave."""
+    cfg = FUSED_EXTRA[name] if name in FUSED_EXTRA else P.CONFIGS[name]
+    desc, blob, offs, w = make_model(cfg, 2, H, W)
+    engine.load_weights(desc, blob, offs)
+    n, d, N = batch * H * W, cfg.dim, cfg.n_experts
+    x = P.synth_features(cfg, batch=batch, H=H, W=W, seed=4).reshape(n, d)
+    aux_n = P.aux_elems(N, n)
+    out = {}
+    for mode in ("stages", "fused"):
+        feats = device_arena(2 * n * d * 2)
+        aux = device_arena(aux_n * 4)
+        hip.upload(feats.ptr, x)
+        hip.memset(aux.ptr, 0xFF, aux_n * 4)  # stale garbage: the launch must not depend on it
+        pa = engine.attn_push(1, 0, n * d, H, W)
+        pr = engine.router_push(1, H * W, n * d, 0, n, n + N)
+        print(f"[attn_route] {name} {H}x{W} batch {batch} {mode}", flush=True)
+        if mode == "stages":
+            assert engine.attn(pa, feats.ptr, batch) == 0, engine.error()
+            assert engine.router(pr, feats.ptr, aux.ptr, batch) == 0, engine.error()
+        else:
+            assert engine.attn_route(pa, pr, feats.ptr, aux.ptr, batch) == 0, engine.error()
+        hip.sync()
+        out[mode] = (hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2),
+                     hip.download(np.empty(aux_n, np.int32), aux.ptr))
+    (hs, auxs), (hf, auxf) = out["stages"], out["fused"]
+    assert (hs == hf).all(), "attention output differs"
+    assert (auxs[:n] == auxf[:n]).all(), "assignment differs"
+    counts = auxf[n:n + N]
+    assert (auxs[n:n + N] == counts).all() and counts.sum() == n
+    perm_s, perm_f = auxs[n + N:].reshape(N, n), auxf[n + N:].reshape(N, n)
+    for e in range(N):
+        assert (np.sort(perm_s[e, :counts[e]]) == np.sort(perm_f[e, :counts[e]])).all(), f"bucket {e}"
+
+
+@pytest.mark.gpu
+def test_attn_route_rejects_mismatched_pushes(hip, engine, device_arena):
+    cfg = P.CONFIGS["moe16"]
+    desc, blob, offs, w = make_model(cfg, 2, 9, 13)
+    engine.load_weights(desc, blob, offs)
+    n, d, N = 117, cfg.dim, cfg.n_experts
+    feats = device_arena(2 * n * d * 2)
+    aux = device_arena(P.aux_elems(N, n) * 4)
+    pa = engine.attn_push(0, 0, n * d, 9, 13)
+    other_block = engine.router_push(1, n, n * d, 0, n, n + N)
+    assert engine.attn_route(pa, other_block, feats.ptr, aux.ptr, 1) == P.ERR_INVALID
+    wrong_input = engine.router_push(0, n, 0, 0, n, n + N)
+    assert engine.attn_route(pa, wrong_input, feats.ptr, aux.ptr, 1) == P.ERR_INVALID
+    assert "attention output" in engine.error()
