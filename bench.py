@@ -38,6 +38,10 @@ def attn_flops_per_token(cfg):
     return 2 * (3 * d * d + 2 * 64 * d + d * d)
 
 
+def router_flops_per_token(cfg):
+    return 2 * cfg.dim * cfg.n_experts if cfg.n_experts > 1 else 0
+
+
 def time_graph(hip, eng, dx, dy, batch, steps, warmup, stream, adapted=False):
     for _ in range(warmup):
         eng.forward(dx, dy, batch, stream, graph=True, adapted=adapted)
@@ -168,13 +172,19 @@ def main():
     e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N)
     log("[bench] per-stage timing")
     t_attn = time_stage(hip, lambda: eng.attn(a_push, feats, B, stream), args.stage_reps, stream)
+    # the chain's MoE-block kernel: attention + routing in one launch (plus the
+    # one-workgroup counter clear the stage call issues before it)
+    rr_push = eng.router_push(0, T, n * d, 0, n, n + N)
+    t_route = time_stage(hip, lambda: eng.attn_route(a_push, rr_push, feats, aux, B, stream), args.stage_reps,
+                         stream)
     # the router launch clears its counts itself; the expert stage only reads them
     t_router = time_stage(hip, lambda: eng.router(r_push, feats, aux, B, stream), args.stage_reps, stream)
     t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, aux, B, stream), args.stage_reps, stream)
-    attn_flops = attn_flops_per_token(cfg) * n
-    attn_tflops = attn_flops / (t_attn * 1e-3) / 1e12
+    route_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * n
+    route_tflops = route_flops / (t_route * 1e-3) / 1e12
     attn_grid = ((cfg.W + 7) // 8) * ((cfg.H + 7) // 8) * B
-    traffic, traffic_src = measured_traffic("prism_attn_d256", attn_grid) if cfg.name == "moe64" else (None, None)
+    kname = "prism_attn_d256_r4"
+    traffic, traffic_src = measured_traffic(kname, attn_grid) if cfg.name == "moe64" else (None, None)
 
     # ---- projection adapters (next to the chain): per launch at batch B, and the
     # adapted chain (up -> blocks -> down) as one graph step
@@ -226,14 +236,15 @@ def main():
         "batch1": {"frames_per_s": round(1e3 / ms_1, 2), "us_per_frame": round(ms_1 * 1e3, 2),
                    "mfma_frac": round(flops_frame / (ms_1 * 1e-3) / MFMA_F16_PEAK, 4),
                    "hbm_frac": round((weight_bytes + io_bytes_1) / (ms_1 * 1e-3) / HBM_PEAK, 4)},
-        "stages_ms": {"attention": round(t_attn, 5), "router": round(t_router, 5), "experts": round(t_expert, 5),
-                      "batch": B},
-        "roofline": {"kernel": "prism_attn_d256", "bound": "mfma", "achieved": round(attn_tflops, 2),
+        "stages_ms": {"attention_routed": round(t_route, 5), "experts": round(t_expert, 5),
+                      "attention_stage": round(t_attn, 5), "router_stage": round(t_router, 5), "batch": B},
+        "roofline": {"kernel": kname, "bound": "mfma", "achieved": round(route_tflops, 2),
                      "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
+                     "frac": round(route_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "traffic_source": traffic_src,
-                     "flops_per_launch": attn_flops, "avg_launch_ms": round(t_attn, 5)},
+                     "flops_per_launch": route_flops, "avg_launch_ms": round(t_route, 5),
+                     "timed": "prism_attn_route stage call: the routed attention kernel + its 1-workgroup counter clear"},
         "expert_load": {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
                         "hottest_share_mean": round(float(share.mean()), 4),
                         "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},
