@@ -260,6 +260,29 @@ int prism_forward_adapted(prism_ctx* ctx, const void* in, void* out, int32_t bat
 int prism_forward_adapted_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch,
                                 void* stream);
 
+/* ---- model files ------------------------------------------------------- */
+
+/* The on-disk model is a pair: <name>.weights, flat fp16 values with no header
+ * (what the reference's exporter writes, vulkan_engine/export_weights.py:
+ * 96-113), and <name>.json, its sidecar ("format": "prism-transformer-v1":
+ * total_fp16_values, total_bytes, the model shape, and one entry per layer with
+ * its kind, block and fp16 element offsets, extending the reference's
+ * per-layer weight_offset_fp16 / bias_offset_fp16 entries, :115-120). Written
+ * by prism-inference_amd/export_weights.py. */
+
+/* Host only: parse and validate a sidecar. offs receives desc->n_blocks
+ * entries (offs_capacity at least that; offs may be NULL to query the shape);
+ * adapters / has_adapters / total_elems may be NULL. */
+int prism_read_model_json(const char* json_path, prism_model_desc* desc, prism_block_offsets* offs,
+                          int32_t offs_capacity, prism_adapter_offsets* adapters, int32_t* has_adapters,
+                          int64_t* total_elems);
+
+/* Load a model pair: sidecar (json_path, or NULL = weights_path with
+ * ".weights" replaced by ".json"), file size checked against it, then the
+ * blocks (prism_load_weights) and, if the sidecar has them, the adapters.
+ * Replaces PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611). */
+int prism_load_model_file(prism_ctx* ctx, const char* weights_path, const char* json_path);
+
 /* aux arena size in int32 elements that a router + expert pair needs for
  * n_experts experts and batch*n_tokens tokens when laid out as
  * [assignment | counts | perm]. */

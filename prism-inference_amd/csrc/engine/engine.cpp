@@ -431,6 +431,38 @@ extern "C" int prism_load_adapters(prism_ctx* c, const void* blob, size_t bytes,
     return PRISM_OK;
 }
 
+extern "C" int prism_load_model_file(prism_ctx* c, const char* weights_path, const char* json_path) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!weights_path) return fail(c, PRISM_ERR_INVALID, "weights_path is NULL");
+    const std::string jp = json_path ? std::string(json_path) : sidecar_path(weights_path);
+    std::string text, why;
+    if (!read_text_file(jp.c_str(), &text)) return fail(c, PRISM_ERR_INVALID, "cannot read %s", jp.c_str());
+    prism_model_desc d{};
+    std::vector<prism_block_offsets> offs;
+    prism_adapter_offsets ad{};
+    bool has_ad = false;
+    int64_t total = 0;
+    int rc = read_model_json(text, &d, &offs, &ad, &has_ad, &total, &why);
+    if (rc) return fail(c, rc, "%s: %s", jp.c_str(), why.c_str());
+    std::ifstream f(weights_path, std::ios::binary | std::ios::ate);
+    if (!f.is_open()) return fail(c, PRISM_ERR_INVALID, "cannot open %s", weights_path);
+    const std::streamsize size = f.tellg();
+    if (size != (std::streamsize)(2 * total))
+        return fail(c, PRISM_ERR_BLOB, "%s holds %lld bytes, its sidecar says %lld", weights_path, (long long)size,
+                    (long long)(2 * total));
+    f.seekg(0);
+    std::vector<char> data;
+    try {
+        data.resize((size_t)size);
+    } catch (...) {
+        return fail(c, PRISM_ERR_NOMEM, "cannot allocate %lld bytes for %s", (long long)size, weights_path);
+    }
+    if (size > 0 && !f.read(data.data(), size)) return fail(c, PRISM_ERR_INVALID, "short read on %s", weights_path);
+    rc = prism_load_weights(c, &d, data.data(), data.size(), offs.data());
+    if (rc) return rc;
+    return has_ad ? prism_load_adapters(c, data.data(), data.size(), &ad) : PRISM_OK;
+}
+
 /* ------------------------------------------------------------ launches */
 
 namespace {

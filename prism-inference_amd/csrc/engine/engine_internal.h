@@ -4,6 +4,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "prism.h"
 
@@ -18,6 +19,12 @@ int validate_adapters(const prism_model_desc* d, const prism_adapter_offsets* a,
 void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst);
 float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);
+
+/* model sidecar (model_file.cpp) */
+int read_model_json(const std::string& text, prism_model_desc* desc, std::vector<prism_block_offsets>* offs,
+                    prism_adapter_offsets* ad, bool* has_adapters, int64_t* total, std::string* why);
+bool read_text_file(const char* path, std::string* out);
+std::string sidecar_path(const char* weights_path);
 
 /* thread-local message for calls that have no context (create, host helpers) */
 void set_global_error(const std::string& msg);

@@ -122,6 +122,9 @@ SIGNATURES = {
     "prism_project_up": (C.c_int, [_P, C.POINTER(ProjectPush), _P, C.c_int32, _P]),
     "prism_project_down": (C.c_int, [_P, C.POINTER(ProjectPush), _P, C.c_int32, _P]),
     "prism_forward_adapted": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_read_model_json": (C.c_int, [C.c_char_p, C.POINTER(ModelDesc), C.POINTER(BlockOffsets), C.c_int32,
+                                        C.POINTER(AdapterOffsets), C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
+    "prism_load_model_file": (C.c_int, [_P, C.c_char_p, C.c_char_p]),
     "prism_forward_adapted_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
 }
 
@@ -260,6 +263,19 @@ def synth_adapters(desc: ModelDesc, seed: int = 0, in_dim: int = ADAPTER_IN, std
     for k, (off, n) in enumerate(((a.up_w, D * in_dim), (a.up_b, D), (a.down_w, in_dim * D), (a.down_b, in_dim))):
         blob[off:off + n] = synth_normal(n, seed=seed, stream=(0xAD << 24) | k, std=std)
     return blob, a
+
+
+def read_model_json(path: str):
+    """(ModelDesc, offsets, AdapterOffsets | None, total fp16 values) from a sidecar."""
+    desc = ModelDesc()
+    _check(lib().prism_read_model_json(path.encode(), C.byref(desc), None, 0, None, None, None))
+    offs = (BlockOffsets * desc.n_blocks)()
+    a = AdapterOffsets()
+    has = C.c_int32()
+    total = C.c_int64()
+    _check(lib().prism_read_model_json(path.encode(), C.byref(desc), offs, desc.n_blocks, C.byref(a), C.byref(has),
+                                       C.byref(total)))
+    return desc, offs, (a if has.value else None), total.value
 
 
 def pack_weight(w: np.ndarray, rows_padded: int | None = None) -> np.ndarray:
@@ -426,6 +442,14 @@ class Engine:
         else:
             f = self.L.prism_forward_graph if graph else self.L.prism_forward
         _check(f(self.h, x, y, batch, stream), self.h)
+
+    def load_model_file(self, weights_path: str, json_path: str | None = None):
+        _check(self.L.prism_load_model_file(self.h, weights_path.encode(),
+                                            json_path.encode() if json_path else None), self.h)
+        desc, offs, a, _ = read_model_json(json_path or weights_path[:-len(".weights")] + ".json")
+        self.desc, self.offs = desc, offs
+        if a is not None:
+            self.aoffs = a
 
     def load_adapters(self, blob: np.ndarray, aoffs: AdapterOffsets):
         blob = np.ascontiguousarray(blob, dtype=np.uint16)
