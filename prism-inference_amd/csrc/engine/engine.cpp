@@ -52,6 +52,12 @@ using namespace prism;
  * routed attention launch adds to them, and counters sharing a cache line
  * would serialise those atomics in one memory channel. */
 static constexpr int CHAIN_COUNT_STRIDE = 64;
+/* From this batch on, the chain runs as two independent half-batch chains on
+ * two streams (two parallel branches of the hipGraph): windows and tokens
+ * never interact across frames, and one half's expert launches overlap the
+ * other half's attention launches and the tails of both. */
+static constexpr int CHAIN_SPLIT = 2;
+static constexpr int CHAIN_SPLIT_MIN_BATCH = 4;
 
 struct prism_ctx {
     int device = 0;
@@ -82,13 +88,15 @@ struct prism_ctx {
     uint16_t* ws_scratch = nullptr;
     uint16_t* ws_io[2] = {};      /* adapted chain: projected input / chain output */
     int32_t* ws_assign = nullptr; /* [n_blocks][n] */
-    int32_t* ws_counts = nullptr; /* [n_blocks][N][CHAIN_COUNT_STRIDE] */
-    int32_t* ws_perm = nullptr;   /* [N][n] */
+    int32_t* ws_counts = nullptr; /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
+    int32_t* ws_perm = nullptr;   /* per half-chain j: [N][its tokens], back to back */
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
 
     hipStream_t cap_stream = nullptr;
+    hipStream_t sub_stream = nullptr; /* second half-chain (default priority) */
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     const void* g_in = nullptr;
@@ -183,10 +191,19 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         }
     }
     e = hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->sub_stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming);
     if (e != hipSuccess) {
+        if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+        if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
+        if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
+    if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
         (void)hipModuleUnload(c->module);
         delete c;
-        return fail(nullptr, PRISM_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+        return fail(nullptr, PRISM_ERR_HIP, "hipStreamCreate / hipEventCreate: %s", hipGetErrorString(e));
     }
     *out = c;
     return PRISM_OK;
@@ -227,6 +244,9 @@ extern "C" void prism_destroy(prism_ctx* c) {
     drop_workspace(c);
     drop_adapters(c);
     if (c->warena) (void)hipFree(c->warena);
+    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
     if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
@@ -768,7 +788,7 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
     const size_t o_attn = ar.take((size_t)n * D * 2);
     const size_t o_scr = ar.take((size_t)n * D * 2);
     const size_t o_asg = ar.take((size_t)NB * n * 4);
-    const size_t o_cnt = ar.take((size_t)NB * N * CHAIN_COUNT_STRIDE * 4);
+    const size_t o_cnt = ar.take((size_t)CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE * 4);
     const size_t o_perm = ar.take((size_t)N * n * 4);
     const size_t o_io0 = ar.take(io ? (size_t)n * D * 2 : 0);
     const size_t o_io1 = ar.take(io ? (size_t)n * D * 2 : 0);
@@ -803,34 +823,40 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
  * row, and the last block clears block 0's for the next chain, so a complete
  * chain leaves row 0 at zero. The workspace starts zeroed; a one-block model
  * clears its row inside the chain; after a chain that failed part-way, the
- * next prism_forward / prism_forward_graph call clears row 0 first. */
-static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
-    const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w;
-    const int64_t n = (int64_t)batch * H * W;
-    const bool moe = c->desc.n_experts > 1;
-    c->fwd_tokens = n;
+ * next prism_forward / prism_forward_graph call clears the counters first.
+ * From CHAIN_SPLIT_MIN_BATCH frames on the batch runs as two half-chains
+ * (own counter rows, own bucket region, disjoint frames of every buffer). */
+static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t* in, uint16_t* out,
+                            hipStream_t s) {
+    const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w, D = c->desc.dim;
     const int N = c->desc.n_experts;
+    const bool moe = N > 1;
+    const int64_t T = (int64_t)H * W, n = (int64_t)nf * T, t0 = (int64_t)f0 * T, n_all = c->fwd_tokens;
     const size_t row = (size_t)N * CHAIN_COUNT_STRIDE;
+    int32_t* counts0 = c->ws_counts + (size_t)j * NB * row;
+    int32_t* perm = c->ws_perm + (size_t)N * t0; /* this half's buckets: [N][n] */
+    uint16_t* attn = c->ws_attn + t0 * D;
+    uint16_t* scratch = c->ws_scratch + t0 * D;
     if (moe && NB == 1) {
-        const int rc = enqueue_zero(c, c->ws_counts, (int32_t)row, s);
+        const int rc = enqueue_zero(c, counts0, (int32_t)row, s);
         if (rc) return rc;
     }
     const uint16_t* src = in;
     for (int b = 0; b < NB; ++b) {
         const DevBlock& k = c->blocks[b];
-        uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : c->ws_scratch;
+        uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : scratch;
         if (moe) {
-            int32_t* counts = c->ws_counts + (size_t)b * row;
-            const RouteOut ro{c->ws_assign + (size_t)b * n, counts, c->ws_perm, CHAIN_COUNT_STRIDE,
-                              NB > 1 ? c->ws_counts + (size_t)((b + 1) % NB) * row : nullptr};
-            int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s, &ro);
+            int32_t* counts = counts0 + (size_t)b * row;
+            const RouteOut ro{c->ws_assign + (size_t)b * n_all + t0, counts, perm, CHAIN_COUNT_STRIDE,
+                              NB > 1 ? counts0 + (size_t)((b + 1) % NB) * row : nullptr};
+            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro);
             if (rc) return rc;
-            rc = enqueue_experts(c, k, c->ws_attn, dst, counts, c->ws_perm, n, s, CHAIN_COUNT_STRIDE);
+            rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE);
             if (rc) return rc;
         } else {
-            int rc = enqueue_attn(c, k, src, c->ws_attn, H, W, batch, s);
+            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s);
             if (rc) return rc;
-            rc = enqueue_experts(c, k, c->ws_attn, dst, nullptr, nullptr, n, s);
+            rc = enqueue_experts(c, k, attn, dst, nullptr, nullptr, n, s);
             if (rc) return rc;
         }
         src = dst;
@@ -838,10 +864,26 @@ static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out,
     return PRISM_OK;
 }
 
+static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
+    const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w, D = c->desc.dim;
+    c->fwd_tokens = (int64_t)batch * T;
+    if (batch < CHAIN_SPLIT_MIN_BATCH) return enqueue_subchain(c, 0, 0, batch, in, out, s);
+    /* fork: frames [fa, batch) on the second stream, [0, fa) on s, then join */
+    const int fa = (batch + 1) / 2, fb = batch - fa;
+    HIP_TRY(c, hipEventRecord(c->ev_fork, s));
+    HIP_TRY(c, hipStreamWaitEvent(c->sub_stream, c->ev_fork, 0));
+    const int rc1 = enqueue_subchain(c, 1, fa, fb, in + fa * T * D, out + fa * T * D, c->sub_stream);
+    HIP_TRY(c, hipEventRecord(c->ev_join, c->sub_stream));
+    const int rc0 = enqueue_subchain(c, 0, 0, fa, in, out, s);
+    HIP_TRY(c, hipStreamWaitEvent(s, c->ev_join, 0));
+    return rc0 ? rc0 : rc1;
+}
+
 /* Clears block 0's counters on `s` if a failed chain may have left them set. */
 static int clean_counts(prism_ctx* c, hipStream_t s) {
     if (!c->counts_dirty || c->desc.n_experts < 2) return PRISM_OK;
-    const int rc = enqueue_zero(c, c->ws_counts, c->desc.n_experts * CHAIN_COUNT_STRIDE, s);
+    /* every half-chain's counter rows (small) */
+    const int rc = enqueue_zero(c, c->ws_counts, CHAIN_SPLIT * c->desc.n_blocks * c->desc.n_experts * CHAIN_COUNT_STRIDE, s);
     if (rc == PRISM_OK) c->counts_dirty = false;
     return rc;
 }

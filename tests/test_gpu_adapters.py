@@ -110,7 +110,7 @@ def test_adapted_chain_needs_adapters(hip, device_arena):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,H,W,batch", [("moe64", 4, 68, 120, 1), ("dense128", 3, 68, 120, 2),
-                                               ("moe16", 2, 20, 28, 3)])
+                                               ("moe16", 2, 20, 28, 3), ("moe16", 2, 20, 28, 4)])
 def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch):
     cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W)
     up_w, up_b, dn_w, dn_b = adapters_f32(desc, ablob, a)

@@ -39,6 +39,8 @@ def setup(hip, engine, name, nb, H, W, seed=0):
     ("dense128", 4, 68, 120, 1),
     ("moe16", 2, 20, 28, 3),
     ("std256", 2, 16, 16, 1),
+    ("moe16", 3, 20, 28, 5),    # two half-chains (3 + 2 frames), parallel graph branches
+    ("dense128", 2, 68, 120, 4),
 ])
 def test_graph_replay_matches_eager(hip, engine, device_arena, name, nb, H, W, batch):
     cfg, desc, blob, offs, w = setup(hip, engine, name, nb, H, W)
