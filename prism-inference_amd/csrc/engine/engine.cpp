@@ -52,12 +52,14 @@ using namespace prism;
  * routed attention launch adds to them, and counters sharing a cache line
  * would serialise those atomics in one memory channel. */
 static constexpr int CHAIN_COUNT_STRIDE = 64;
-/* From this batch on, the chain runs as two independent half-batch chains on
- * two streams (two parallel branches of the hipGraph): windows and tokens
- * never interact across frames, and one half's expert launches overlap the
- * other half's attention launches and the tails of both. */
+/* The chain runs as up to CHAIN_SPLIT independent sub-chains, one per
+ * CHAIN_SPLIT_FRAMES frames, on their own streams (parallel branches of the
+ * hipGraph): windows and tokens never interact across frames, and one
+ * sub-chain's expert launches overlap another's attention launches and the
+ * tails of both. */
 static constexpr int CHAIN_SPLIT = 2;
-static constexpr int CHAIN_SPLIT_MIN_BATCH = 4;
+static constexpr int CHAIN_SPLIT_FRAMES = 2;
+static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
 
 struct prism_ctx {
     int device = 0;
@@ -95,8 +97,8 @@ struct prism_ctx {
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
 
     hipStream_t cap_stream = nullptr;
-    hipStream_t sub_stream = nullptr; /* second half-chain (default priority) */
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    hipStream_t sub_stream[3] = {};   /* sub-chains 1.. (default priority) */
+    hipEvent_t ev_fork = nullptr, ev_join[3] = {};
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     const void* g_in = nullptr;
@@ -191,16 +193,18 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         }
     }
     e = hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->sub_stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming);
+    for (int j = 0; j + 1 < CHAIN_SPLIT && e == hipSuccess; ++j) {
+        e = hipStreamCreateWithFlags(&c->sub_stream[j], hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_join[j], hipEventDisableTiming);
+    }
     if (e != hipSuccess) {
+        for (int j = 0; j + 1 < CHAIN_SPLIT; ++j) {
+            if (c->ev_join[j]) (void)hipEventDestroy(c->ev_join[j]);
+            if (c->sub_stream[j]) (void)hipStreamDestroy(c->sub_stream[j]);
+        }
         if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-        if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
-        if (c->ev_join) (void)hipEventDestroy(c->ev_join);
-    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-    if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
-    if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
+        if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
         (void)hipModuleUnload(c->module);
         delete c;
         return fail(nullptr, PRISM_ERR_HIP, "hipStreamCreate / hipEventCreate: %s", hipGetErrorString(e));
@@ -244,9 +248,11 @@ extern "C" void prism_destroy(prism_ctx* c) {
     drop_workspace(c);
     drop_adapters(c);
     if (c->warena) (void)hipFree(c->warena);
-    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    for (int j = 0; j + 1 < CHAIN_SPLIT; ++j) {
+        if (c->ev_join[j]) (void)hipEventDestroy(c->ev_join[j]);
+        if (c->sub_stream[j]) (void)hipStreamDestroy(c->sub_stream[j]);
+    }
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-    if (c->sub_stream) (void)hipStreamDestroy(c->sub_stream);
     if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
@@ -824,7 +830,7 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
  * chain leaves row 0 at zero. The workspace starts zeroed; a one-block model
  * clears its row inside the chain; after a chain that failed part-way, the
  * next prism_forward / prism_forward_graph call clears the counters first.
- * From CHAIN_SPLIT_MIN_BATCH frames on the batch runs as two half-chains
+ * With 2 * CHAIN_SPLIT_FRAMES frames or more the batch runs as sub-chains
  * (own counter rows, own bucket region, disjoint frames of every buffer). */
 static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t* in, uint16_t* out,
                             hipStream_t s) {
@@ -867,16 +873,21 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
 static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
     const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w, D = c->desc.dim;
     c->fwd_tokens = (int64_t)batch * T;
-    if (batch < CHAIN_SPLIT_MIN_BATCH) return enqueue_subchain(c, 0, 0, batch, in, out, s);
-    /* fork: frames [fa, batch) on the second stream, [0, fa) on s, then join */
-    const int fa = (batch + 1) / 2, fb = batch - fa;
+    const int S = std::max(1, std::min(CHAIN_SPLIT, batch / CHAIN_SPLIT_FRAMES));
+    if (S == 1) return enqueue_subchain(c, 0, 0, batch, in, out, s);
+    /* fork: sub-chain j > 0 on sub_stream[j-1], sub-chain 0 on s, then join */
     HIP_TRY(c, hipEventRecord(c->ev_fork, s));
-    HIP_TRY(c, hipStreamWaitEvent(c->sub_stream, c->ev_fork, 0));
-    const int rc1 = enqueue_subchain(c, 1, fa, fb, in + fa * T * D, out + fa * T * D, c->sub_stream);
-    HIP_TRY(c, hipEventRecord(c->ev_join, c->sub_stream));
-    const int rc0 = enqueue_subchain(c, 0, 0, fa, in, out, s);
-    HIP_TRY(c, hipStreamWaitEvent(s, c->ev_join, 0));
-    return rc0 ? rc0 : rc1;
+    int rc = PRISM_OK;
+    for (int j = S - 1; j >= 0; --j) {
+        const int f0 = (int)((int64_t)batch * j / S), f1 = (int)((int64_t)batch * (j + 1) / S);
+        hipStream_t sj = j ? c->sub_stream[j - 1] : s;
+        if (j) HIP_TRY(c, hipStreamWaitEvent(sj, c->ev_fork, 0));
+        const int r = enqueue_subchain(c, j, f0, f1 - f0, in + f0 * T * D, out + f0 * T * D, sj);
+        if (!rc) rc = r;
+        if (j) HIP_TRY(c, hipEventRecord(c->ev_join[j - 1], sj));
+    }
+    for (int j = 1; j < S; ++j) HIP_TRY(c, hipStreamWaitEvent(s, c->ev_join[j - 1], 0));
+    return rc;
 }
 
 /* Clears block 0's counters on `s` if a failed chain may have left them set. */
