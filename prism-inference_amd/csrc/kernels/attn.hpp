@@ -92,12 +92,15 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     __shared__ __attribute__((aligned(16))) f16 os[64 * LDS];
     __shared__ float s_bqkv[3 * DIM];
     __shared__ float s_bo[DIM];
-    __shared__ float s_g[DIM];          /* LN1, then LN2 (routing) */
+    __shared__ float s_g[DIM];          /* LN1 */
     __shared__ float s_b[DIM];
+    constexpr int RDIM = NPT > 0 ? DIM : 1;
+    __shared__ float s_g2[RDIM];        /* LN2 (routing) */
+    __shared__ float s_b2[RDIM];
+    __shared__ float s_br[NPT > 0 ? 16 * NPT : 1]; /* router bias */
     /* routing scratch aliases the QKV biases, dead after the barrier ahead of
      * the out-proj */
     static_assert(3 * DIM >= 5 * 64, "routing scratch fits the QKV bias area");
-    float* const r_br = s_bqkv;                           /* [16*NPT] router bias    */
     int* const r_hist = reinterpret_cast<int*>(s_bqkv) + 64; /* [64] window histogram */
     int* const r_base = r_hist + 64;                     /* [64] bucket bases        */
     int* const r_e = r_base + 64;                        /* [64] expert per slot     */
@@ -124,7 +127,27 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     const bool routes = NPT > 0 && wave < 4;
     const int total = routes ? S::TOTAL : S::RBASE;
 
-    /* weight ring: first PF fragments go out before anything else */
+    /* ---- 1. LN1 --------------------------------------------------------
+     * The window's rows (HBM) are requested first, then the weight ring and
+     * the parameters (L2). Loads complete in issue order, so the first wait
+     * for a parameter also covers the rows: one memory round trip before
+     * the math, not two. */
+    constexpr int LPS = DIM / 16;
+    constexpr int SPI = 64 / LPS;       /* slots per wave iteration */
+    constexpr int SPW = 64 / NW;        /* slots per wave           */
+    constexpr int IT = SPW / SPI;
+    RowChunk rc[IT];
+    bool valid[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int s = wave * SPW + it * SPI + lane / LPS;
+        const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
+        valid[it] = gy < a.H && gx < a.W;
+        rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
+    }
+    sched_fence();
+
+    /* weight ring: the first PF fragments */
     h8 ring[PF];
 #pragma unroll
     for (int p = 0; p < PF; ++p) ring[p] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p, loff);
@@ -134,33 +157,24 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
      * block's expert stage of the previous chain, has finished) */
     if (NPT > 0 && a.zero_next && blockIdx.x == 0 && threadIdx.x < a.n_experts)
         a.zero_next[threadIdx.x * a.count_stride] = 0;
+    /* every parameter is staged now: a load issued after the residual
+     * prefetch below would make its LDS store wait for that HBM fetch */
     for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
     for (int i = threadIdx.x; i < DIM; i += NT) {
         s_bo[i] = a.bo[i];
         s_g[i] = a.ln_g[i];
         s_b[i] = a.ln_b[i];
-    }
-
-    /* ---- 1. LN1: all row loads first, then the math ------------------ */
-    {
-        constexpr int LPS = DIM / 16;
-        constexpr int SPI = 64 / LPS;   /* slots per wave iteration */
-        constexpr int SPW = 64 / NW;    /* slots per wave           */
-        constexpr int IT = SPW / SPI;
-        RowChunk rc[IT];
-        bool valid[IT];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int s = wave * SPW + it * SPI + lane / LPS;
-            const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-            valid[it] = gy < a.H && gx < a.W;
-            rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
+        if constexpr (NPT > 0) {
+            s_g2[i] = a.ln2_g[i];
+            s_b2[i] = a.ln2_b[i];
         }
-        __syncthreads(); /* LN parameters staged */
-#pragma unroll
-        for (int it = 0; it < IT; ++it)
-            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * SPW + it * SPI + lane / LPS) * LDS, nullptr);
     }
+    if constexpr (NPT > 0)
+        for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
+    __syncthreads(); /* parameters staged */
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+        ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * SPW + it * SPI + lane / LPS) * LDS, nullptr);
     __syncthreads();
 
     /* ---- 2./3. per head ----------------------------------------------- */
@@ -307,18 +321,9 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
         for (int r = 0; r < ORT; ++r)
             xin[t][r] = *reinterpret_cast<const h4*>(in + tbase[t] + (wave * ORT + r) * 16 + 4 * g);
     }
-    if constexpr (NPT > 0) {
-        /* LN1's parameters are dead (every wave passed the barrier after LN1) */
-        for (int i = threadIdx.x; i < DIM; i += NT) {
-            s_g[i] = a.ln2_g[i];
-            s_b[i] = a.ln2_b[i];
-        }
-    }
     __syncthreads();
-    if constexpr (NPT > 0) { /* the QKV biases are dead now */
-        for (int i = threadIdx.x; i < 16 * NPT; i += NT) r_br[i] = a.br[i];
+    if constexpr (NPT > 0) /* the QKV biases are dead now */
         if (threadIdx.x < 64) r_hist[threadIdx.x] = 0;
-    }
 
     /* ---- 4. out-proj + residual --------------------------------------- */
     f4 acc[ORT][4]; /* starts at the out-proj bias */
@@ -376,7 +381,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             h8 cur[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(xs + sl * LDS + 32 * ks + 8 * g);
-            const int e = route_token<DIM, NPT>(cur, s_g, s_b, r_br, g, a.n_experts, [&](int rt, int ks) {
+            const int e = route_token<DIM, NPT>(cur, s_g2, s_b2, s_br, g, a.n_experts, [&](int rt, int ks) {
                 const int p = S::RBASE + ks * NPT + rt;
                 const h8 w = ring[p % PF];
                 if (p + PF < S::TOTAL)
