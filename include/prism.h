@@ -283,6 +283,42 @@ int prism_read_model_json(const char* json_path, prism_model_desc* desc, prism_b
  * Replaces PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611). */
 int prism_load_model_file(prism_ctx* ctx, const char* weights_path, const char* json_path);
 
+/* ---- host renderer interop ---------------------------------------------- */
+
+/* PrismVulkan::InitWithDevice (vulkan_engine/prism_vulkan.h:81-85,
+ * prism_vulkan.cpp:27-48): an engine on the renderer's device and queue.
+ * Here: prism_create on `device`, bound to the renderer's stream (a
+ * hipStream_t of that device; NULL = the null stream), on which
+ * prism_infer_gpu runs. A stream of another device is refused. */
+int prism_init_with_device(prism_ctx** out, int32_t device, void* stream, const char* code_object_path);
+
+/* PrismVulkan::InferGPU (prism_vulkan.h:93-98, prism_vulkan.cpp:922-1005): one
+ * inference from caller device memory to caller device memory at byte offsets
+ * into the caller's buffers, then wait for it. *infer_ms (may be NULL)
+ * receives the inference's GPU time (HIP events around the graph launch).
+ * Zero-copy: the kernels read in_buf + in_offset and write out_buf +
+ * out_offset themselves, where the reference copies through its own feature
+ * buffer. Runs the block chain's hipGraph (captured on the first call for a
+ * given pair of addresses) on the bound stream: the adapted chain, in/out
+ * [batch][H*W][in_dim], when adapters are loaded, else the blocks,
+ * [batch][H*W][dim]. Both addresses 16-byte aligned; the two ranges must not
+ * overlap. */
+int prism_infer_gpu(prism_ctx* ctx, const void* in_buf, uint64_t in_offset, void* out_buf, uint64_t out_offset,
+                    int32_t batch, float* infer_ms);
+
+/* Renderer-owned memory as engine buffers: import an allocation exported as an
+ * opaque file descriptor (a VkDeviceMemory exported through
+ * VK_KHR_external_memory_fd, or any dma-buf of this device) and map its first
+ * `size` bytes as a device pointer for prism_infer_gpu / prism_forward. The
+ * caller keeps its descriptor (the library imports a duplicate and closes
+ * that at release). Release waits for the device, then unmaps. No reference
+ * counterpart: the reference shares the renderer's VkDevice and VkBuffers
+ * directly. */
+typedef struct prism_external_buffer prism_external_buffer;
+int prism_import_external_memory(prism_ctx* ctx, int32_t fd, uint64_t size, prism_external_buffer** buf,
+                                 void** dev_ptr);
+int prism_release_external_memory(prism_ctx* ctx, prism_external_buffer* buf);
+
 /* aux arena size in int32 elements that a router + expert pair needs for
  * n_experts experts and batch*n_tokens tokens when laid out as
  * [assignment | counts | perm]. */

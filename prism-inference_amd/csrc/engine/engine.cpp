@@ -11,9 +11,12 @@
  * buffer that is re-submitted every frame, prism_moe_bench.cpp:183-209).
  */
 #include <dlfcn.h>
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -95,6 +98,9 @@ struct prism_ctx {
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
+
+    hipStream_t user_stream = nullptr;  /* prism_init_with_device: the renderer's stream */
+    hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr; /* prism_infer_gpu timing */
 
     hipStream_t cap_stream = nullptr;
     hipStream_t sub_stream[3] = {};   /* sub-chains 1.. (default priority) */
@@ -194,6 +200,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
     }
     e = hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreate(&c->ev_t0);
+    if (e == hipSuccess) e = hipEventCreate(&c->ev_t1);
     for (int j = 0; j + 1 < CHAIN_SPLIT && e == hipSuccess; ++j) {
         e = hipStreamCreateWithFlags(&c->sub_stream[j], hipStreamNonBlocking);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_join[j], hipEventDisableTiming);
@@ -204,6 +212,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
             if (c->sub_stream[j]) (void)hipStreamDestroy(c->sub_stream[j]);
         }
         if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+        if (c->ev_t0) (void)hipEventDestroy(c->ev_t0);
+        if (c->ev_t1) (void)hipEventDestroy(c->ev_t1);
         if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
         (void)hipModuleUnload(c->module);
         delete c;
@@ -253,6 +263,8 @@ extern "C" void prism_destroy(prism_ctx* c) {
         if (c->sub_stream[j]) (void)hipStreamDestroy(c->sub_stream[j]);
     }
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->ev_t0) (void)hipEventDestroy(c->ev_t0);
+    if (c->ev_t1) (void)hipEventDestroy(c->ev_t1);
     if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
@@ -935,7 +947,11 @@ static int run_forward(prism_ctx* c, const void* in, void* out, int32_t batch, v
     return rc;
 }
 
-static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted) {
+/* `before`, if given, is recorded on the stream right before the graph launch
+ * (after any capture and counter clear), so its distance to an event recorded
+ * after the call is the chain's GPU time alone. */
+static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted,
+                             hipEvent_t before = nullptr) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
     if (adapted && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
@@ -969,6 +985,7 @@ static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t ba
     }
     rc = clean_counts(c, (hipStream_t)stream);
     if (rc) return rc;
+    if (before) HIP_TRY(c, hipEventRecord(before, (hipStream_t)stream));
     HIP_TRY(c, hipGraphLaunch(c->gexec, (hipStream_t)stream));
     return PRISM_OK;
 }
@@ -994,5 +1011,113 @@ extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_de
     if (!c->ws) return fail(c, PRISM_ERR_STATE, "no forward has run");
     if (assign_dev) *assign_dev = c->ws_assign;
     if (tokens_per_block) *tokens_per_block = c->fwd_tokens;
+    return PRISM_OK;
+}
+
+/* ------------------------------------------------------------ host renderer interop */
+
+extern "C" int prism_init_with_device(prism_ctx** out, int32_t device, void* stream, const char* code_object_path) {
+    const int rc = prism_create(out, device, code_object_path);
+    if (rc) return rc;
+    prism_ctx* c = *out;
+    if (stream) {
+        int sdev = -1;
+        const hipError_t e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+        if (e != hipSuccess || sdev != device) {
+            prism_destroy(c);
+            *out = nullptr;
+            return fail(nullptr, PRISM_ERR_INVALID, "stream is not a stream of device %d (%s, device %d)", device,
+                        hipGetErrorString(e), sdev);
+        }
+    }
+    c->user_stream = (hipStream_t)stream;
+    return PRISM_OK;
+}
+
+extern "C" int prism_infer_gpu(prism_ctx* c, const void* in_buf, uint64_t in_offset, void* out_buf,
+                               uint64_t out_offset, int32_t batch, float* infer_ms) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!in_buf || !out_buf) return fail(c, PRISM_ERR_INVALID, "in_buf or out_buf is NULL");
+    if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
+    if (batch < 1) return fail(c, PRISM_ERR_INVALID, "batch %d < 1", batch);
+    const bool adapted = c->adapters;
+    const int64_t ch = adapted ? c->aoffs.in_dim : c->desc.dim;
+    const uint64_t bytes = (uint64_t)batch * c->desc.spatial_h * c->desc.spatial_w * ch * 2;
+    const char* in = static_cast<const char*>(in_buf) + in_offset;
+    char* out = static_cast<char*>(out_buf) + out_offset;
+    if (in < out + bytes && out < in + bytes)
+        return fail(c, PRISM_ERR_INVALID, "input and output ranges overlap (%llu bytes each)",
+                    (unsigned long long)bytes);
+    int rc = run_forward_graph(c, in, out, batch, c->user_stream, adapted, c->ev_t0);
+    if (rc) return rc;
+    HIP_TRY(c, hipEventRecord(c->ev_t1, c->user_stream));
+    HIP_TRY(c, hipEventSynchronize(c->ev_t1));
+    float ms = 0.f;
+    HIP_TRY(c, hipEventElapsedTime(&ms, c->ev_t0, c->ev_t1));
+    if (infer_ms) *infer_ms = ms;
+    return PRISM_OK;
+}
+
+struct prism_external_buffer {
+    hipExternalMemory_t mem;
+    void* ptr;
+    int fd;     /* the library's duplicate of the caller's descriptor */
+    int device;
+};
+
+extern "C" int prism_import_external_memory(prism_ctx* c, int32_t fd, uint64_t size, prism_external_buffer** buf,
+                                            void** dev_ptr) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!buf || !dev_ptr) return fail(c, PRISM_ERR_INVALID, "buf or dev_ptr is NULL");
+    *buf = nullptr;
+    *dev_ptr = nullptr;
+    if (fd < 0) return fail(c, PRISM_ERR_INVALID, "fd %d is not a descriptor", fd);
+    if (size == 0) return fail(c, PRISM_ERR_INVALID, "size is 0");
+    const int dfd = fcntl(fd, F_DUPFD_CLOEXEC, 0);
+    if (dfd < 0) return fail(c, PRISM_ERR_INVALID, "fd %d: %s", fd, strerror(errno));
+    hipError_t e = hipSetDevice(c->device);
+    hipExternalMemory_t mem = nullptr;
+    if (e == hipSuccess) {
+        hipExternalMemoryHandleDesc d;
+        memset(&d, 0, sizeof d);
+        d.type = hipExternalMemoryHandleTypeOpaqueFd;
+        d.handle.fd = dfd;
+        d.size = size;
+        e = hipImportExternalMemory(&mem, &d);
+    }
+    if (e != hipSuccess) {
+        close(dfd);
+        return fail(c, PRISM_ERR_HIP, "hipImportExternalMemory(fd %d, %llu bytes): %s", fd, (unsigned long long)size,
+                    hipGetErrorString(e));
+    }
+    hipExternalMemoryBufferDesc bd;
+    memset(&bd, 0, sizeof bd);
+    bd.offset = 0;
+    bd.size = size;
+    void* p = nullptr;
+    e = hipExternalMemoryGetMappedBuffer(&p, mem, &bd);
+    if (e != hipSuccess || !p) {
+        (void)hipDestroyExternalMemory(mem);
+        close(dfd);
+        return fail(c, PRISM_ERR_HIP, "hipExternalMemoryGetMappedBuffer: %s", hipGetErrorString(e));
+    }
+    *buf = new prism_external_buffer{mem, p, dfd, c->device};
+    *dev_ptr = p;
+    return PRISM_OK;
+}
+
+extern "C" int prism_release_external_memory(prism_ctx* c, prism_external_buffer* b) {
+    if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
+    if (!b) return fail(c, PRISM_ERR_INVALID, "buffer is NULL");
+    HIP_TRY(c, hipSetDevice(b->device));
+    /* work still reading or writing the buffer must end before its mapping does */
+    const hipError_t es = hipDeviceSynchronize();
+    const hipError_t ef = hipFree(b->ptr);
+    const hipError_t ed = hipDestroyExternalMemory(b->mem);
+    close(b->fd);
+    delete b;
+    if (es != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipDeviceSynchronize: %s", hipGetErrorString(es));
+    if (ef != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipFree(mapped buffer): %s", hipGetErrorString(ef));
+    if (ed != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipDestroyExternalMemory: %s", hipGetErrorString(ed));
     return PRISM_OK;
 }

@@ -126,6 +126,10 @@ SIGNATURES = {
                                         C.POINTER(AdapterOffsets), C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
     "prism_load_model_file": (C.c_int, [_P, C.c_char_p, C.c_char_p]),
     "prism_forward_adapted_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_init_with_device": (C.c_int, [C.POINTER(_P), C.c_int32, _P, C.c_char_p]),
+    "prism_infer_gpu": (C.c_int, [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_int32, C.POINTER(C.c_float)]),
+    "prism_import_external_memory": (C.c_int, [_P, C.c_int32, C.c_uint64, C.POINTER(_P), C.POINTER(_P)]),
+    "prism_release_external_memory": (C.c_int, [_P, _P]),
 }
 
 _lib = None
@@ -387,10 +391,15 @@ class Hip:
 class Engine:
     """One prism_ctx: weights on the device and the stage / chain launches."""
 
-    def __init__(self, device: int = 0, code_object: str | None = None):
+    def __init__(self, device: int = 0, code_object: str | None = None, stream: int | None = None):
+        """prism_create, or prism_init_with_device when a renderer stream is given."""
         self.L = lib()
         h = C.c_void_p()
-        rc = self.L.prism_create(C.byref(h), device, code_object.encode() if code_object else None)
+        co = code_object.encode() if code_object else None
+        if stream is None:
+            rc = self.L.prism_create(C.byref(h), device, co)
+        else:
+            rc = self.L.prism_init_with_device(C.byref(h), device, stream, co)
         _check(rc, None)
         self.h = h
         self.desc = None
@@ -442,6 +451,21 @@ class Engine:
         else:
             f = self.L.prism_forward_graph if graph else self.L.prism_forward
         _check(f(self.h, x, y, batch, stream), self.h)
+
+    def infer_gpu(self, in_buf: int, in_offset: int, out_buf: int, out_offset: int, batch: int) -> float:
+        """prism_infer_gpu: one synchronous inference between caller buffers; returns GPU ms."""
+        ms = C.c_float()
+        _check(self.L.prism_infer_gpu(self.h, in_buf, in_offset, out_buf, out_offset, batch, C.byref(ms)), self.h)
+        return ms.value
+
+    def import_external_memory(self, fd: int, size: int):
+        """(handle, device pointer) of an exported allocation's first `size` bytes."""
+        buf, ptr = C.c_void_p(), C.c_void_p()
+        _check(self.L.prism_import_external_memory(self.h, fd, size, C.byref(buf), C.byref(ptr)), self.h)
+        return buf, ptr.value
+
+    def release_external_memory(self, buf):
+        _check(self.L.prism_release_external_memory(self.h, buf), self.h)
 
     def load_model_file(self, weights_path: str, json_path: str | None = None):
         _check(self.L.prism_load_model_file(self.h, weights_path.encode(),

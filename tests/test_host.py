@@ -213,7 +213,22 @@ def test_context_calls_fail_cleanly_without_a_context():
     assert L.prism_project_down(None, C.byref(P.ProjectPush()), None, 1, None) == P.ERR_INVALID
     assert L.prism_forward_adapted(None, None, None, 1, None) == P.ERR_INVALID
     assert L.prism_forward_adapted_graph(None, None, None, 1, None) == P.ERR_INVALID
+    ms = C.c_float()
+    assert L.prism_infer_gpu(None, None, 0, None, 0, 1, C.byref(ms)) == P.ERR_INVALID
+    buf, ptr = C.c_void_p(), C.c_void_p()
+    assert L.prism_import_external_memory(None, 0, 1, C.byref(buf), C.byref(ptr)) == P.ERR_INVALID
+    assert L.prism_release_external_memory(None, None) == P.ERR_INVALID
     L.prism_destroy(None)  # no-op
+
+
+def test_init_with_device_without_a_gpu_fails_cleanly():
+    """No device in this process (or a device index past the last): an error
+    code and a message, no context."""
+    L = P.lib()
+    h = C.c_void_p(1)
+    rc = L.prism_init_with_device(C.byref(h), 4096, None, None)
+    assert rc in (P.ERR_HIP, P.ERR_INVALID) and h.value is None
+    assert L.prism_last_error(None)
 
 
 @pytest.mark.parametrize("name", ["moe64", "dense128"])
