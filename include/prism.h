@@ -283,6 +283,66 @@ int prism_read_model_json(const char* json_path, prism_model_desc* desc, prism_b
  * Replaces PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611). */
 int prism_load_model_file(prism_ctx* ctx, const char* weights_path, const char* json_path);
 
+/* ---- conv encoder / fused decoder (the end-to-end frame) ---------------- */
+
+/* The end-to-end frame of prism_moe_bench.cpp:387-466 around the blocks:
+ *   encoder  enc0 conv3x3 9->32 (render resolution r0), enc1 conv3x3/2 32->64
+ *            (r1), enc2 conv3x3/2 64->128 (r2), enc3 conv3x3/2 128->128 (r3 =
+ *            the token grid), each + ReLU;
+ *   [adapters + blocks on the r3 tokens];
+ *   decoder  dec3 NN-up + concat enc2 -> PW 256->128 (r2), dec2 NN-up + concat
+ *            enc1 -> PW 192->64 (r1), dec1 NN-up + concat enc0 -> PW 96->32
+ *            (r0), each + ReLU; output PW 32->12; PixelShuffle(2) + sigmoid
+ *            -> RGB at 2 x r0.
+ * r(i+1) = ceil(r(i) / 2) and r3 must be the model's spatial_h x spatial_w.
+ * Weight offsets (fp16 elements, 8-aligned), row-major [out][in] with the
+ * reference's column orders: conv k = ic*9 + ky*3 + kx (enc*), concat order
+ * upsampled channels first (dec*). */
+typedef struct prism_codec_offsets {
+    int32_t render_w, render_h; /* r0, e.g. 960 x 540 */
+    int32_t in_channels, scale; /* 9 and 2 (the only values supported) */
+    int64_t enc0_w, enc0_b, enc1_w, enc1_b, enc2_w, enc2_b, enc3_w, enc3_b;
+    int64_t dec3_w, dec3_b, dec2_w, dec2_b, dec1_w, dec1_b, out_w, out_b;
+} prism_codec_offsets;
+
+/* Place the encoder, the adapters and the decoder in a blob from element
+ * `base` on, in the reference's wa() order (prism_moe_bench.cpp:347-357:
+ * enc_ic, enc1, enc2, enc3, proj_up, proj_dn, d3_pw, d2_pw, d1_pw, out_pw);
+ * *end = first element past them. adapters may be NULL. Host only. */
+int prism_codec_layout(const prism_model_desc* desc, int32_t render_w, int32_t render_h, int64_t base,
+                       prism_codec_offsets* codec, prism_adapter_offsets* adapters, int64_t* end);
+
+/* Upload the encoder and decoder weights (host fp16 blob, `bytes` long) for
+ * the loaded model; loading weights of another shape drops them. */
+int prism_load_codec(prism_ctx* ctx, const void* blob, size_t bytes, const prism_codec_offsets* offs);
+
+/* The encoder: frame fp16 CHW [batch][9][render_h][render_w] -> bottleneck
+ * fp16 [batch][r3 tokens][128] (token-major, the adapted chain's input). The
+ * encoder maps stay in the engine for the next prism_decode of `batch`
+ * frames. */
+int prism_encode(prism_ctx* ctx, const void* frame, void* bottleneck, int32_t batch, void* stream);
+
+/* The decoder: bottleneck fp16 [batch][r3 tokens][128] -> display fp16 CHW
+ * [batch][3][2 render_h][2 render_w], with the skips of the last
+ * prism_encode (same batch). */
+int prism_decode(prism_ctx* ctx, const void* bottleneck, void* display, int32_t batch, void* stream);
+
+/* One codec stage on caller buffers, for stage-level checks: stage 0..3 =
+ * enc0..enc3 (in: the CHW frame for stage 0, else the previous NHWC map;
+ * skip unused), 4 = dec3, 5 = dec2 (in: the coarse NHWC map, skip: the
+ * encoder map of the output resolution), 6 = dec1 + output conv +
+ * PixelShuffle + sigmoid (out: the CHW display image). Maps between stages
+ * are NHWC fp16 [batch][pixels][channels]. */
+int prism_codec_stage(prism_ctx* ctx, int32_t stage, const void* in, const void* skip, void* out, int32_t batch,
+                      void* stream);
+
+/* The whole end-to-end frame: encoder, up-projection, every block,
+ * down-projection, decoder (needs the codec and the adapters loaded).
+ * frame: [batch][9][render_h][render_w], display: [batch][3][2 render_h]
+ * [2 render_w], both fp16 CHW. _graph replays a captured hipGraph. */
+int prism_forward_e2e(prism_ctx* ctx, const void* frame, void* display, int32_t batch, void* stream);
+int prism_forward_e2e_graph(prism_ctx* ctx, const void* frame, void* display, int32_t batch, void* stream);
+
 /* ---- host renderer interop ---------------------------------------------- */
 
 /* PrismVulkan::InitWithDevice (vulkan_engine/prism_vulkan.h:81-85,
@@ -298,11 +358,12 @@ int prism_init_with_device(prism_ctx** out, int32_t device, void* stream, const 
  * receives the inference's GPU time (HIP events around the graph launch).
  * Zero-copy: the kernels read in_buf + in_offset and write out_buf +
  * out_offset themselves, where the reference copies through its own feature
- * buffer. Runs the block chain's hipGraph (captured on the first call for a
- * given pair of addresses) on the bound stream: the adapted chain, in/out
- * [batch][H*W][in_dim], when adapters are loaded, else the blocks,
- * [batch][H*W][dim]. Both addresses 16-byte aligned; the two ranges must not
- * overlap. */
+ * buffer. Runs a captured hipGraph (captured on the first call for a given
+ * pair of addresses) on the bound stream: the whole end-to-end frame (frame
+ * in, display out, as prism_forward_e2e) when the codec and adapters are
+ * loaded, else the adapted chain, in/out [batch][H*W][in_dim], when adapters
+ * are loaded, else the blocks, [batch][H*W][dim]. Both addresses 16-byte
+ * aligned; the two ranges must not overlap. */
 int prism_infer_gpu(prism_ctx* ctx, const void* in_buf, uint64_t in_offset, void* out_buf, uint64_t out_offset,
                     int32_t batch, float* infer_ms);
 

@@ -400,6 +400,149 @@ int oracle_project(const float* W, const float* b, int in_dim, int out_dim, int 
     return 0;
 }
 
+/* ---- conv encoder / fused decoder (the end-to-end frame around the blocks,
+ * prism_moe_bench.cpp:387-466). Maps are CHW, as the shaders keep them. */
+
+/* conv3x3, padding 1, stride s: y[oc][oy][ox] = r16(b[oc] + sum W[oc][ic*9 +
+ * ky*3 + kx] x[ic][oy*s + ky - 1][ox*s + kx - 1]) (zero outside the map), then
+ * ReLU if relu. conv3x3_coopvec_9ch.comp.glsl:27-72 (s = 1, relu flag),
+ * strided_conv_coopvec_32ch.comp.glsl:30-77 and strided_conv_split_{64,128}ch
+ * .comp.glsl:30-94 (s = 2, ReLU). The split shaders round each 288-column
+ * partial sum to fp16 before adding them; their comments state the result is
+ * the unsplit conv's, which is what this computes (one rounding of the full
+ * sum). Output oh = (h - 1) / s + 1, ow = (w - 1) / s + 1. */
+int oracle_conv3x3(const float* x, int cin, int h, int w, int stride, const float* W, const float* b, int cout,
+                   int relu, int faithful, float* y) {
+    if (!x || !W || !b || !y || cin <= 0 || cout <= 0 || h <= 0 || w <= 0 || (stride != 1 && stride != 2))
+        return -1;
+    const int oh = (h - 1) / stride + 1, ow = (w - 1) / stride + 1;
+    const int K = cin * 9, Kp = (K + 7) & ~7;
+    float* Wp = (float*)calloc((size_t)cout * Kp, sizeof(float));
+    if (!Wp) return -2;
+    for (int o = 0; o < cout; ++o) memcpy(Wp + (size_t)o * Kp, W + (size_t)o * K, sizeof(float) * K);
+    int rc = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (int oy = 0; oy < oh; ++oy) {
+        float* P = (float*)calloc((size_t)ow * Kp, sizeof(float));
+        float* R = (float*)malloc(sizeof(float) * (size_t)ow * cout);
+        if (!P || !R) {
+            free(P);
+            free(R);
+#pragma omp atomic write
+            rc = -2;
+            continue;
+        }
+        for (int ox = 0; ox < ow; ++ox)
+            for (int ic = 0; ic < cin; ++ic)
+                for (int t = 0; t < 9; ++t) {
+                    const int iy = oy * stride + t / 3 - 1, ix = ox * stride + t % 3 - 1;
+                    if (iy >= 0 && iy < h && ix >= 0 && ix < w)
+                        P[(size_t)ox * Kp + ic * 9 + t] = x[((size_t)ic * h + iy) * w + ix];
+                }
+        gemm_xwT(P, ow, Kp, Wp, b, cout, R, cout, faithful);
+        for (int ox = 0; ox < ow; ++ox)
+            for (int o = 0; o < cout; ++o) {
+                const float v = R[(size_t)ox * cout + o];
+                y[((size_t)o * oh + oy) * ow + ox] = relu && v < 0.f ? 0.f : v;
+            }
+        free(P);
+        free(R);
+    }
+    free(Wp);
+    return rc;
+}
+
+/* Fused decoder stage (dec3_fused.comp.glsl:27-63, dec{2,1}_fused.comp.glsl:
+ * 27-55): in = concat(up[c][min(oy/2, uh-1)][min(ox/2, uw-1)] for c < cup,
+ * skip[c][oy][ox] for c < cskip); y[o][oy][ox] = ReLU(r16(W[o] . in + b[o])).
+ * W is [cout][cup + cskip]; cup + cskip must be a multiple of 8. */
+int oracle_dec_stage(const float* up, int cup, int uh, int uw, const float* skip, int cskip, int oh, int ow,
+                     const float* W, const float* b, int cout, int faithful, float* y) {
+    const int K = cup + cskip;
+    if (!up || !skip || !W || !b || !y || cup <= 0 || cskip <= 0 || K % 8 || uh <= 0 || uw <= 0 || oh <= 0 ||
+        ow <= 0)
+        return -1;
+    int rc = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (int oy = 0; oy < oh; ++oy) {
+        float* P = (float*)malloc(sizeof(float) * (size_t)ow * K);
+        float* R = (float*)malloc(sizeof(float) * (size_t)ow * cout);
+        if (!P || !R) {
+            free(P);
+            free(R);
+#pragma omp atomic write
+            rc = -2;
+            continue;
+        }
+        const int uy = oy / 2 < uh - 1 ? oy / 2 : uh - 1;
+        for (int ox = 0; ox < ow; ++ox) {
+            const int ux = ox / 2 < uw - 1 ? ox / 2 : uw - 1;
+            for (int c = 0; c < cup; ++c) P[(size_t)ox * K + c] = up[((size_t)c * uh + uy) * uw + ux];
+            for (int c = 0; c < cskip; ++c) P[(size_t)ox * K + cup + c] = skip[((size_t)c * oh + oy) * ow + ox];
+        }
+        gemm_xwT(P, ow, K, W, b, cout, R, cout, faithful);
+        for (int ox = 0; ox < ow; ++ox)
+            for (int o = 0; o < cout; ++o) {
+                const float v = R[(size_t)ox * cout + o];
+                y[((size_t)o * oh + oy) * ow + ox] = v < 0.f ? 0.f : v;
+            }
+        free(P);
+        free(R);
+    }
+    return rc;
+}
+
+/* Pointwise conv (pw_conv_coopvec_32to12.comp.glsl:28-55): y[o][p] =
+ * r16(W[o] . x[:, p] + b[o]), ReLU if relu. cin % 8 == 0. */
+int oracle_pw_conv(const float* x, int cin, int h, int w, const float* W, const float* b, int cout, int relu,
+                   int faithful, float* y) {
+    if (!x || !W || !b || !y || cin <= 0 || cin % 8 || cout <= 0 || h <= 0 || w <= 0) return -1;
+    const size_t n = (size_t)h * w;
+    int rc = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (int yy = 0; yy < h; ++yy) {
+        float* P = (float*)malloc(sizeof(float) * (size_t)w * cin);
+        float* R = (float*)malloc(sizeof(float) * (size_t)w * cout);
+        if (!P || !R) {
+            free(P);
+            free(R);
+#pragma omp atomic write
+            rc = -2;
+            continue;
+        }
+        for (int xx = 0; xx < w; ++xx)
+            for (int c = 0; c < cin; ++c) P[(size_t)xx * cin + c] = x[(size_t)c * n + (size_t)yy * w + xx];
+        gemm_xwT(P, w, cin, W, b, cout, R, cout, faithful);
+        for (int xx = 0; xx < w; ++xx)
+            for (int o = 0; o < cout; ++o) {
+                const float v = R[(size_t)xx * cout + o];
+                y[(size_t)o * n + (size_t)yy * w + xx] = relu && v < 0.f ? 0.f : v;
+            }
+        free(P);
+        free(R);
+    }
+    return rc;
+}
+
+/* PixelShuffle(s) + sigmoid (pixelshuffle_sigmoid.comp.glsl:28-56): display
+ * pixel (oy, ox) of RGB plane c reads channel c*s*s + (oy%s)*s + (ox%s) at
+ * (oy/s, ox/s); y = r16(1 / (1 + exp(-x))). x is [3*s*s][h][w], y is
+ * [3][s*h][s*w]. */
+int oracle_pixelshuffle_sigmoid(const float* x, int h, int w, int s, int faithful, float* y) {
+    if (!x || !y || h <= 0 || w <= 0 || s < 1) return -1;
+    const int dh = h * s, dw = w * s;
+    const size_t rp = (size_t)h * w;
+#pragma omp parallel for
+    for (int oy = 0; oy < dh; ++oy)
+        for (int c = 0; c < 3; ++c)
+            for (int ox = 0; ox < dw; ++ox) {
+                const int src = c * s * s + (oy % s) * s + ox % s;
+                const float v = x[(size_t)src * rp + (size_t)(oy / s) * w + ox / s];
+                y[((size_t)c * dh + oy) * dw + ox] = rnd(faithful, 1.0f / (1.0f + expf(-v)));
+            }
+    return 0;
+}
+
 int oracle_forward(const oracle_cfg* c, const float* w, const oracle_block_offsets* offs,
                    int n_blocks, const float* x, float* y, int32_t* assign_out, float* h_out) {
     if (check_cfg(c) || !w || !offs || !x || !y || n_blocks <= 0) return -1;

@@ -13,6 +13,12 @@
  *   shaders/moe_expert_skip.comp.glsl:25-54       expert stage
  *   shaders/pw_project_128to256.comp.glsl:25-37   projection 128 -> 256 + ReLU
  *   shaders/pw_project_256to128.comp.glsl:25-32   projection 256 -> 128
+ *   shaders/conv3x3_coopvec_9ch.comp.glsl:27-72   encoder input conv
+ *   shaders/strided_conv_coopvec_32ch.comp.glsl:30-77, strided_conv_split_{64,128}ch
+ *                                                 stride-2 encoder convs
+ *   shaders/dec{3,2,1}_fused.comp.glsl            fused decoder stages
+ *   shaders/pw_conv_coopvec_32to12.comp.glsl:28-55 output conv
+ *   shaders/pixelshuffle_sigmoid.comp.glsl:28-56  PixelShuffle + sigmoid
  *   vulkan_engine/prism_moe_bench.cpp:164-172     weight offset layout
  *   vulkan_engine/prism_moe_bench.cpp:262-291     per-block host order
  *
@@ -89,6 +95,15 @@ int oracle_forward(const oracle_cfg* c, const float* w,
  * W is [out_dim][in_dim]; in_dim % 8 == 0. */
 int oracle_project(const float* W, const float* b, int in_dim, int out_dim, int relu, const float* x,
                    int n, int faithful, float* y);
+
+/* Encoder / decoder stages on CHW maps (oracle.c has the formulas). */
+int oracle_conv3x3(const float* x, int cin, int h, int w, int stride, const float* W, const float* b, int cout,
+                   int relu, int faithful, float* y);
+int oracle_dec_stage(const float* up, int cup, int uh, int uw, const float* skip, int cskip, int oh, int ow,
+                     const float* W, const float* b, int cout, int faithful, float* y);
+int oracle_pw_conv(const float* x, int cin, int h, int w, const float* W, const float* b, int cout, int relu,
+                   int faithful, float* y);
+int oracle_pixelshuffle_sigmoid(const float* x, int h, int w, int s, int faithful, float* y);
 
 int oracle_max_threads(void);
 void oracle_set_threads(int n);

@@ -50,6 +50,11 @@ def lib():
         L.oracle_gelu.argtypes = [_F, _F, C.c_size_t]
         L.oracle_project.argtypes = [_F, _F, C.c_int, C.c_int, C.c_int, _F, C.c_int, C.c_int, _F]
         L.oracle_window_attention.argtypes = [C.POINTER(Cfg), _F, _F, _F, _F]
+        L.oracle_conv3x3.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int, _F]
+        L.oracle_dec_stage.argtypes = [_F, C.c_int, C.c_int, C.c_int, _F, C.c_int, C.c_int, C.c_int, _F, _F,
+                                       C.c_int, C.c_int, _F]
+        L.oracle_pw_conv.argtypes = [_F, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int, _F]
+        L.oracle_pixelshuffle_sigmoid.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F]
         L.oracle_f16_to_f32.argtypes = [C.POINTER(C.c_uint16), _F, C.c_size_t]
         L.oracle_f32_to_f16.argtypes = [_F, C.POINTER(C.c_uint16), C.c_size_t]
         L.oracle_max_threads.restype = C.c_int
@@ -193,3 +198,49 @@ def max_threads() -> int:
 
 def set_threads(n: int):
     lib().oracle_set_threads(n)
+
+
+# ---- conv encoder / fused decoder, CHW maps -------------------------------
+
+def conv3x3(x: np.ndarray, W: np.ndarray, b: np.ndarray, stride: int, relu: bool = True,
+            faithful: bool = True) -> np.ndarray:
+    """x [cin][h][w], W [cout][cin*9] (k = ic*9 + ky*3 + kx) -> [cout][oh][ow]."""
+    cin, h, w = x.shape
+    cout = W.shape[0]
+    oh, ow = (h - 1) // stride + 1, (w - 1) // stride + 1
+    x, W, b = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, W, b))
+    y = np.empty((cout, oh, ow), np.float32)
+    _chk(lib().oracle_conv3x3(_f(x), cin, h, w, stride, _f(W), _f(b), cout, int(relu), int(faithful), _f(y)),
+         "oracle_conv3x3")
+    return y
+
+
+def dec_stage(up: np.ndarray, skip: np.ndarray, W: np.ndarray, b: np.ndarray, faithful: bool = True) -> np.ndarray:
+    """up [cup][uh][uw], skip [cskip][oh][ow], W [cout][cup+cskip] -> [cout][oh][ow] (ReLU)."""
+    cup, uh, uw = up.shape
+    cskip, oh, ow = skip.shape
+    cout = W.shape[0]
+    up, skip, W, b = (np.ascontiguousarray(a, dtype=np.float32) for a in (up, skip, W, b))
+    y = np.empty((cout, oh, ow), np.float32)
+    _chk(lib().oracle_dec_stage(_f(up), cup, uh, uw, _f(skip), cskip, oh, ow, _f(W), _f(b), cout, int(faithful),
+                                _f(y)), "oracle_dec_stage")
+    return y
+
+
+def pw_conv(x: np.ndarray, W: np.ndarray, b: np.ndarray, relu: bool = False, faithful: bool = True) -> np.ndarray:
+    cin, h, w = x.shape
+    cout = W.shape[0]
+    x, W, b = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, W, b))
+    y = np.empty((cout, h, w), np.float32)
+    _chk(lib().oracle_pw_conv(_f(x), cin, h, w, _f(W), _f(b), cout, int(relu), int(faithful), _f(y)),
+         "oracle_pw_conv")
+    return y
+
+
+def pixelshuffle_sigmoid(x: np.ndarray, s: int = 2, faithful: bool = True) -> np.ndarray:
+    c, h, w = x.shape
+    assert c == 3 * s * s
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty((3, h * s, w * s), np.float32)
+    _chk(lib().oracle_pixelshuffle_sigmoid(_f(x), h, w, s, int(faithful), _f(y)), "oracle_pixelshuffle_sigmoid")
+    return y

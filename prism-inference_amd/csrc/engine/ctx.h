@@ -1,0 +1,134 @@
+/* ctx.h - the engine context and helpers shared by the host engine's
+ * translation units (engine.cpp, codec.cpp). */
+#ifndef PRISM_CTX_H
+#define PRISM_CTX_H
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../kernel_args.h"
+#include "prism.h"
+
+namespace prism {
+
+struct DevBlock {
+    prism_block_offsets offs;
+    uint16_t* wqkv;
+    float* bqkv;
+    uint16_t* wo;
+    float* bo;
+    float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+    uint16_t* wr;
+    float* br;
+    uint16_t* w1;
+    float* b1;
+    uint16_t* w2;
+    float* b2;
+};
+
+}  // namespace prism
+
+using prism::DevBlock;
+
+/* The chain's per-expert counters sit 256 bytes apart: every workgroup of a
+ * routed attention launch adds to them, and counters sharing a cache line
+ * would serialise those atomics in one memory channel. */
+static constexpr int CHAIN_COUNT_STRIDE = 64;
+/* The chain runs as up to CHAIN_SPLIT independent sub-chains, one per
+ * CHAIN_SPLIT_FRAMES frames, on their own streams (parallel branches of the
+ * hipGraph): windows and tokens never interact across frames, and one
+ * sub-chain's expert launches overlap another's attention launches and the
+ * tails of both. */
+static constexpr int CHAIN_SPLIT = 2;
+static constexpr int CHAIN_SPLIT_FRAMES = 2;
+static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
+
+enum ChainMode { CHAIN_BLOCKS = 0, CHAIN_ADAPTED = 1, CHAIN_E2E = 2 };
+
+struct prism_ctx {
+    int device = 0;
+    hipModule_t module = nullptr;
+    hipFunction_t f_attn[2][2][5] = {}; /* [d128, d256][4 waves, 8 waves][routed: padded experts / 16] */
+    hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
+    hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
+    hipFunction_t f_zero = nullptr;
+    hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */
+    hipFunction_t f_codec[7] = {};     /* enc0..enc3, dec3, dec2, dec1_out */
+    std::string err;
+
+    bool loaded = false;
+    prism_model_desc desc{};
+    void* warena = nullptr;
+    std::vector<DevBlock> blocks;
+
+    /* projection adapters (prism_load_adapters) */
+    void* aarena = nullptr;
+    bool adapters = false;
+    prism_adapter_offsets aoffs{};
+    uint16_t *up_w = nullptr, *down_w = nullptr; /* packed */
+    float *up_b = nullptr, *down_b = nullptr;
+
+    /* forward workspace */
+    void* ws = nullptr;
+    int ws_batch = 0;
+    uint16_t* ws_attn = nullptr;
+    uint16_t* ws_scratch = nullptr;
+    uint16_t* ws_io[2] = {};      /* adapted chain: projected input / chain output */
+    int32_t* ws_assign = nullptr; /* [n_blocks][n] */
+    int32_t* ws_counts = nullptr; /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
+    int32_t* ws_perm = nullptr;   /* per half-chain j: [N][its tokens], back to back */
+    int64_t ws_tokens = 0;
+    int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
+    bool counts_dirty = false;    /* block 0's counters may be nonzero */
+
+    hipStream_t user_stream = nullptr;  /* prism_init_with_device: the renderer's stream */
+    hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr; /* prism_infer_gpu timing */
+
+    hipStream_t cap_stream = nullptr;
+    hipStream_t sub_stream[3] = {};   /* sub-chains 1.. (default priority) */
+    hipEvent_t ev_fork = nullptr, ev_join[3] = {};
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    const void* g_in = nullptr;
+    void* g_out = nullptr;
+    int g_batch = 0;
+    int g_mode = 0;               /* ChainMode of the captured graph */
+
+    /* conv encoder / fused decoder (codec.cpp) */
+    bool codec = false;
+    prism_codec_offsets coffs{};
+    void* carena = nullptr;       /* packed stage weights + fp32 biases */
+    const uint16_t* cw[8] = {};   /* enc0..enc3, dec3, dec2, dec1, out (packed) */
+    const float* cb[8] = {};
+    int cr_w[4] = {}, cr_h[4] = {}; /* r0 (render) .. r3 (= the token grid) */
+    void* cws = nullptr;          /* codec workspace for cws_batch frames */
+    int cws_batch = 0;
+    uint16_t *ce0 = nullptr, *ce1 = nullptr, *ce2 = nullptr; /* encoder maps kept for the decoder's skips */
+    uint16_t *cbott = nullptr, *cchain = nullptr;             /* bottleneck in / chain out (e2e) */
+    uint16_t *cd3 = nullptr, *cd2 = nullptr;
+};
+
+/* Record the message on the context (if any) and the thread; returns code. */
+int fail(prism_ctx* c, int code, const char* fmt, ...);
+
+#define HIP_TRY(ctx, call)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail((ctx), PRISM_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+/* engine.cpp: forget the captured chain graph */
+void drop_graph(prism_ctx* c);
+
+/* codec.cpp: the conv encoder / fused decoder stages on a stream */
+void codec_release(prism_ctx* c);
+int codec_ensure_workspace(prism_ctx* c, int batch);
+int codec_enqueue_encode(prism_ctx* c, const uint16_t* frame, uint16_t* bottleneck, int batch, hipStream_t s);
+int codec_enqueue_decode(prism_ctx* c, const uint16_t* bottleneck, uint16_t* display, int batch, hipStream_t s);
+int64_t codec_frame_elems(const prism_ctx* c);   /* 9 * render_h * render_w */
+int64_t codec_display_elems(const prism_ctx* c); /* 3 * (2 render_h) * (2 render_w) */
+
+#endif

@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "../kernel_args.h"
+#include "ctx.h"
 #include "engine_internal.h"
 
 namespace prism {
@@ -32,88 +33,11 @@ namespace prism {
 static thread_local std::string g_error;
 void set_global_error(const std::string& msg) { g_error = msg; }
 
-struct DevBlock {
-    prism_block_offsets offs;
-    uint16_t* wqkv;
-    float* bqkv;
-    uint16_t* wo;
-    float* bo;
-    float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
-    uint16_t* wr;
-    float* br;
-    uint16_t* w1;
-    float* b1;
-    uint16_t* w2;
-    float* b2;
-};
-
 }  // namespace prism
 
 using namespace prism;
 
-/* The chain's per-expert counters sit 256 bytes apart: every workgroup of a
- * routed attention launch adds to them, and counters sharing a cache line
- * would serialise those atomics in one memory channel. */
-static constexpr int CHAIN_COUNT_STRIDE = 64;
-/* The chain runs as up to CHAIN_SPLIT independent sub-chains, one per
- * CHAIN_SPLIT_FRAMES frames, on their own streams (parallel branches of the
- * hipGraph): windows and tokens never interact across frames, and one
- * sub-chain's expert launches overlap another's attention launches and the
- * tails of both. */
-static constexpr int CHAIN_SPLIT = 2;
-static constexpr int CHAIN_SPLIT_FRAMES = 2;
-static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
-
-struct prism_ctx {
-    int device = 0;
-    hipModule_t module = nullptr;
-    hipFunction_t f_attn[2][2][5] = {}; /* [d128, d256][4 waves, 8 waves][routed: padded experts / 16] */
-    hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
-    hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
-    hipFunction_t f_zero = nullptr;
-    hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */
-    std::string err;
-
-    bool loaded = false;
-    prism_model_desc desc{};
-    void* warena = nullptr;
-    std::vector<DevBlock> blocks;
-
-    /* projection adapters (prism_load_adapters) */
-    void* aarena = nullptr;
-    bool adapters = false;
-    prism_adapter_offsets aoffs{};
-    uint16_t *up_w = nullptr, *down_w = nullptr; /* packed */
-    float *up_b = nullptr, *down_b = nullptr;
-
-    /* forward workspace */
-    void* ws = nullptr;
-    int ws_batch = 0;
-    uint16_t* ws_attn = nullptr;
-    uint16_t* ws_scratch = nullptr;
-    uint16_t* ws_io[2] = {};      /* adapted chain: projected input / chain output */
-    int32_t* ws_assign = nullptr; /* [n_blocks][n] */
-    int32_t* ws_counts = nullptr; /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
-    int32_t* ws_perm = nullptr;   /* per half-chain j: [N][its tokens], back to back */
-    int64_t ws_tokens = 0;
-    int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
-    bool counts_dirty = false;    /* block 0's counters may be nonzero */
-
-    hipStream_t user_stream = nullptr;  /* prism_init_with_device: the renderer's stream */
-    hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr; /* prism_infer_gpu timing */
-
-    hipStream_t cap_stream = nullptr;
-    hipStream_t sub_stream[3] = {};   /* sub-chains 1.. (default priority) */
-    hipEvent_t ev_fork = nullptr, ev_join[3] = {};
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t gexec = nullptr;
-    const void* g_in = nullptr;
-    void* g_out = nullptr;
-    int g_batch = 0;
-    bool g_adapted = false;
-};
-
-static int fail(prism_ctx* c, int code, const char* fmt, ...) {
+int fail(prism_ctx* c, int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -123,13 +47,6 @@ static int fail(prism_ctx* c, int code, const char* fmt, ...) {
     g_error = buf;
     return code;
 }
-
-#define HIP_TRY(ctx, call)                                                                   \
-    do {                                                                                     \
-        hipError_t e_ = (call);                                                              \
-        if (e_ != hipSuccess)                                                                \
-            return fail((ctx), PRISM_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
-    } while (0)
 
 static int dim_index(int dim) { return dim == 256 ? 1 : 0; }
 
@@ -181,6 +98,10 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_zero, "prism_zero_i32"},
         {&c->f_proj[0][0], "prism_project_up_d128"},   {&c->f_proj[0][1], "prism_project_down_d128"},
         {&c->f_proj[1][0], "prism_project_up_d256"},   {&c->f_proj[1][1], "prism_project_down_d256"},
+        {&c->f_codec[0], "prism_codec_enc0"}, {&c->f_codec[1], "prism_codec_enc1"},
+        {&c->f_codec[2], "prism_codec_enc2"}, {&c->f_codec[3], "prism_codec_enc3"},
+        {&c->f_codec[4], "prism_codec_dec3"}, {&c->f_codec[5], "prism_codec_dec2"},
+        {&c->f_codec[6], "prism_codec_dec1_out"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);
@@ -223,7 +144,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
     return PRISM_OK;
 }
 
-static void drop_graph(prism_ctx* c) {
+void drop_graph(prism_ctx* c) {
     if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
     c->gexec = nullptr;
@@ -231,7 +152,7 @@ static void drop_graph(prism_ctx* c) {
     c->g_in = nullptr;
     c->g_out = nullptr;
     c->g_batch = 0;
-    c->g_adapted = false;
+    c->g_mode = CHAIN_BLOCKS;
 }
 
 static void drop_adapters(prism_ctx* c) {
@@ -257,6 +178,7 @@ extern "C" void prism_destroy(prism_ctx* c) {
     drop_graph(c);
     drop_workspace(c);
     drop_adapters(c);
+    codec_release(c);
     if (c->warena) (void)hipFree(c->warena);
     for (int j = 0; j + 1 < CHAIN_SPLIT; ++j) {
         if (c->ev_join[j]) (void)hipEventDestroy(c->ev_join[j]);
@@ -402,6 +324,7 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
         c->desc.spatial_h != d->spatial_h || c->desc.spatial_w != d->spatial_w)
         drop_workspace(c);
     if (c->desc.dim != d->dim) drop_adapters(c);
+    if (c->desc.spatial_h != d->spatial_h || c->desc.spatial_w != d->spatial_w) codec_release(c);
     c->desc = *d;
     c->loaded = true;
     return PRISM_OK;
@@ -920,10 +843,18 @@ static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
     return PRISM_OK;
 }
 
-/* The chain, optionally wrapped in the projection adapters: up(in ->
- * ws_io[0]), blocks(ws_io[0] -> ws_io[1]), down(ws_io[1] -> out). */
-static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, bool adapted, hipStream_t s) {
-    if (!adapted) return enqueue_forward_impl(c, in, out, batch, s);
+/* The chain (CHAIN_BLOCKS); wrapped in the projection adapters (CHAIN_ADAPTED):
+ * up(in -> ws_io[0]), blocks(ws_io[0] -> ws_io[1]), down(ws_io[1] -> out);
+ * and that inside the encoder and decoder (CHAIN_E2E): encode(frame ->
+ * cbott), adapted chain(cbott -> cchain), decode(cchain -> display). */
+static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, int mode, hipStream_t s) {
+    if (mode == CHAIN_BLOCKS) return enqueue_forward_impl(c, in, out, batch, s);
+    if (mode == CHAIN_E2E) {
+        int rc = codec_enqueue_encode(c, in, c->cbott, batch, s);
+        if (!rc) rc = enqueue_chain(c, c->cbott, c->cchain, batch, CHAIN_ADAPTED, s);
+        if (!rc) rc = codec_enqueue_decode(c, c->cchain, out, batch, s);
+        return rc;
+    }
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
     int rc = enqueue_project(c, true, in, c->ws_io[0], n, s);
     if (rc) return rc;
@@ -932,16 +863,23 @@ static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int ba
     return enqueue_project(c, false, c->ws_io[1], out, n, s);
 }
 
-static int run_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted) {
+static int mode_ready(prism_ctx* c, int mode, int batch) {
+    if (mode != CHAIN_BLOCKS && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
+    if (mode == CHAIN_E2E && !c->codec) return fail(c, PRISM_ERR_STATE, "encoder / decoder weights not loaded");
+    int rc = ensure_workspace(c, batch, mode != CHAIN_BLOCKS);
+    if (!rc && mode == CHAIN_E2E) rc = codec_ensure_workspace(c, batch);
+    return rc;
+}
+
+static int run_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, int mode) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
-    if (adapted && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
     HIP_TRY(c, hipSetDevice(c->device));
-    rc = ensure_workspace(c, batch, adapted);
+    rc = mode_ready(c, mode, batch);
     if (rc) return rc;
     rc = clean_counts(c, (hipStream_t)stream);
     if (rc) return rc;
-    rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, adapted,
+    rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, mode,
                        (hipStream_t)stream);
     if (rc) c->counts_dirty = true; /* launched part of the chain */
     return rc;
@@ -950,20 +888,19 @@ static int run_forward(prism_ctx* c, const void* in, void* out, int32_t batch, v
 /* `before`, if given, is recorded on the stream right before the graph launch
  * (after any capture and counter clear), so its distance to an event recorded
  * after the call is the chain's GPU time alone. */
-static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, bool adapted,
+static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream, int mode,
                              hipEvent_t before = nullptr) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
-    if (adapted && !c->adapters) return fail(c, PRISM_ERR_STATE, "adapters not loaded");
     HIP_TRY(c, hipSetDevice(c->device));
-    if (!(c->gexec && c->g_in == in && c->g_out == out && c->g_batch == batch && c->g_adapted == adapted)) {
-        rc = ensure_workspace(c, batch, adapted);
-        if (rc) return rc;
+    rc = mode_ready(c, mode, batch); /* may reallocate (which drops the graph) */
+    if (rc) return rc;
+    if (!(c->gexec && c->g_in == in && c->g_out == out && c->g_batch == batch && c->g_mode == mode)) {
         drop_graph(c);
         HIP_TRY(c, hipStreamSynchronize(c->cap_stream));
         HIP_TRY(c, hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
         /* captured, not run: a failure here leaves the counters untouched */
-        rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, adapted,
+        rc = enqueue_chain(c, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, mode,
                            c->cap_stream);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(c->cap_stream, &g);
@@ -981,7 +918,7 @@ static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t ba
         c->g_in = in;
         c->g_out = out;
         c->g_batch = batch;
-        c->g_adapted = adapted;
+        c->g_mode = mode;
     }
     rc = clean_counts(c, (hipStream_t)stream);
     if (rc) return rc;
@@ -991,19 +928,27 @@ static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t ba
 }
 
 extern "C" int prism_forward(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
-    return run_forward(c, in, out, batch, stream, false);
+    return run_forward(c, in, out, batch, stream, CHAIN_BLOCKS);
 }
 
 extern "C" int prism_forward_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
-    return run_forward_graph(c, in, out, batch, stream, false);
+    return run_forward_graph(c, in, out, batch, stream, CHAIN_BLOCKS);
 }
 
 extern "C" int prism_forward_adapted(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
-    return run_forward(c, in, out, batch, stream, true);
+    return run_forward(c, in, out, batch, stream, CHAIN_ADAPTED);
 }
 
 extern "C" int prism_forward_adapted_graph(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
-    return run_forward_graph(c, in, out, batch, stream, true);
+    return run_forward_graph(c, in, out, batch, stream, CHAIN_ADAPTED);
+}
+
+extern "C" int prism_forward_e2e(prism_ctx* c, const void* frame, void* display, int32_t batch, void* stream) {
+    return run_forward(c, frame, display, batch, stream, CHAIN_E2E);
+}
+
+extern "C" int prism_forward_e2e_graph(prism_ctx* c, const void* frame, void* display, int32_t batch, void* stream) {
+    return run_forward_graph(c, frame, display, batch, stream, CHAIN_E2E);
 }
 
 extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_dev, int64_t* tokens_per_block) {
@@ -1040,15 +985,19 @@ extern "C" int prism_infer_gpu(prism_ctx* c, const void* in_buf, uint64_t in_off
     if (!in_buf || !out_buf) return fail(c, PRISM_ERR_INVALID, "in_buf or out_buf is NULL");
     if (!c->loaded) return fail(c, PRISM_ERR_STATE, "weights not loaded");
     if (batch < 1) return fail(c, PRISM_ERR_INVALID, "batch %d < 1", batch);
-    const bool adapted = c->adapters;
-    const int64_t ch = adapted ? c->aoffs.in_dim : c->desc.dim;
-    const uint64_t bytes = (uint64_t)batch * c->desc.spatial_h * c->desc.spatial_w * ch * 2;
+    const int mode = c->adapters ? (c->codec ? CHAIN_E2E : CHAIN_ADAPTED) : CHAIN_BLOCKS;
+    const uint64_t tok = (uint64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
+    uint64_t in_bytes = tok * (mode == CHAIN_ADAPTED ? c->aoffs.in_dim : c->desc.dim) * 2, out_bytes = in_bytes;
+    if (mode == CHAIN_E2E) {
+        in_bytes = (uint64_t)batch * codec_frame_elems(c) * 2;
+        out_bytes = (uint64_t)batch * codec_display_elems(c) * 2;
+    }
     const char* in = static_cast<const char*>(in_buf) + in_offset;
     char* out = static_cast<char*>(out_buf) + out_offset;
-    if (in < out + bytes && out < in + bytes)
-        return fail(c, PRISM_ERR_INVALID, "input and output ranges overlap (%llu bytes each)",
-                    (unsigned long long)bytes);
-    int rc = run_forward_graph(c, in, out, batch, c->user_stream, adapted, c->ev_t0);
+    if (in < out + out_bytes && out < in + in_bytes)
+        return fail(c, PRISM_ERR_INVALID, "input and output ranges overlap (%llu / %llu bytes)",
+                    (unsigned long long)in_bytes, (unsigned long long)out_bytes);
+    int rc = run_forward_graph(c, in, out, batch, c->user_stream, mode, c->ev_t0);
     if (rc) return rc;
     HIP_TRY(c, hipEventRecord(c->ev_t1, c->user_stream));
     HIP_TRY(c, hipEventSynchronize(c->ev_t1));

@@ -16,6 +16,10 @@ int validate_blocks(const prism_model_desc* d, const prism_block_offsets* offs, 
                     std::string* why);
 int validate_adapters(const prism_model_desc* d, const prism_adapter_offsets* a, int64_t total,
                       std::string* why);
+int validate_codec(const prism_model_desc* d, const prism_codec_offsets* c, int64_t total, std::string* why);
+/* r0 (render) .. r3 (the token grid) of a render size; false (why) if r3 is
+ * not the model's grid */
+bool codec_resolutions(const prism_model_desc* d, int render_w, int render_h, int* rw, int* rh, std::string* why);
 void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst);
 float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);

@@ -260,6 +260,120 @@ extern "C" int prism_adapter_layout(const prism_model_desc* desc, int32_t in_dim
     return PRISM_OK;
 }
 
+/* Encoder / decoder tensor table: name, offset, element count. */
+struct CodecTensor {
+    const char* name;
+    int64_t off, n;
+};
+
+static int codec_tensors(const prism_codec_offsets* c, CodecTensor* t) {
+    const CodecTensor v[] = {
+        {"enc0_w", c->enc0_w, 32 * 81},   {"enc0_b", c->enc0_b, 32},   {"enc1_w", c->enc1_w, 64 * 288},
+        {"enc1_b", c->enc1_b, 64},        {"enc2_w", c->enc2_w, 128 * 576}, {"enc2_b", c->enc2_b, 128},
+        {"enc3_w", c->enc3_w, 128 * 1152}, {"enc3_b", c->enc3_b, 128}, {"dec3_w", c->dec3_w, 128 * 256},
+        {"dec3_b", c->dec3_b, 128},       {"dec2_w", c->dec2_w, 64 * 192}, {"dec2_b", c->dec2_b, 64},
+        {"dec1_w", c->dec1_w, 32 * 96},   {"dec1_b", c->dec1_b, 32},   {"out_w", c->out_w, 12 * 32},
+        {"out_b", c->out_b, 12},
+    };
+    const int n = (int)(sizeof v / sizeof v[0]);
+    for (int i = 0; i < n; ++i) t[i] = v[i];
+    return n;
+}
+
+bool prism::codec_resolutions(const prism_model_desc* d, int render_w, int render_h, int* rw, int* rh,
+                              std::string* why) {
+    if (render_w < 1 || render_h < 1 || render_w > 16384 || render_h > 16384) {
+        if (why) *why = "render size " + std::to_string(render_w) + "x" + std::to_string(render_h) + " out of range";
+        return false;
+    }
+    rw[0] = render_w;
+    rh[0] = render_h;
+    for (int i = 1; i < 4; ++i) { /* a 3x3 stride-2 conv with padding 1 */
+        rw[i] = (rw[i - 1] + 1) / 2;
+        rh[i] = (rh[i - 1] + 1) / 2;
+    }
+    if (rw[3] != d->spatial_w || rh[3] != d->spatial_h) {
+        if (why)
+            *why = "render size " + std::to_string(render_w) + "x" + std::to_string(render_h) + " encodes to " +
+                   std::to_string(rw[3]) + "x" + std::to_string(rh[3]) + ", the model's token grid is " +
+                   std::to_string(d->spatial_w) + "x" + std::to_string(d->spatial_h);
+        return false;
+    }
+    return true;
+}
+
+int prism::validate_codec(const prism_model_desc* d, const prism_codec_offsets* c, int64_t total, std::string* why) {
+    if (!shape_supported(d, why)) return PRISM_ERR_UNSUPPORTED;
+    if (!c) { if (why) *why = "codec offsets are NULL"; return PRISM_ERR_INVALID; }
+    if (c->in_channels != 9 || c->scale != 2) {
+        if (why)
+            *why = "codec in_channels " + std::to_string(c->in_channels) + ", scale " + std::to_string(c->scale) +
+                   " (supported: 9 and 2)";
+        return PRISM_ERR_UNSUPPORTED;
+    }
+    int rw[4], rh[4];
+    if (!codec_resolutions(d, c->render_w, c->render_h, rw, rh, why)) return PRISM_ERR_INVALID;
+    CodecTensor t[16];
+    const int n = codec_tensors(c, t);
+    for (int i = 0; i < n; ++i)
+        if (!span_ok(t[i].off, t[i].n, total)) {
+            if (why) *why = std::string("codec ") + t[i].name + " outside the blob or not 8-aligned";
+            return PRISM_ERR_BLOB;
+        }
+    return PRISM_OK;
+}
+
+extern "C" int prism_codec_layout(const prism_model_desc* desc, int32_t render_w, int32_t render_h, int64_t base,
+                                  prism_codec_offsets* c, prism_adapter_offsets* ad, int64_t* end) {
+    std::string why;
+    if (!shape_supported(desc, &why)) {
+        set_global_error(why);
+        return PRISM_ERR_UNSUPPORTED;
+    }
+    int rw[4], rh[4];
+    if (!c || base < 0) {
+        set_global_error("prism_codec_layout: codec offsets NULL or base < 0");
+        return PRISM_ERR_INVALID;
+    }
+    if (!codec_resolutions(desc, render_w, render_h, rw, rh, &why)) {
+        set_global_error(why);
+        return PRISM_ERR_INVALID;
+    }
+    /* enc_ic, enc1, enc2, enc3, proj_up, proj_dn, d3_pw, d2_pw, d1_pw, out_pw
+     * (prism_moe_bench.cpp:347-357) */
+    int64_t cur = (base + 7) & ~int64_t(7);
+    const int64_t D = desc->dim, I = 128;
+    c->render_w = render_w;
+    c->render_h = render_h;
+    c->in_channels = 9;
+    c->scale = 2;
+    c->enc0_w = bump(cur, 32 * 81);
+    c->enc0_b = bump(cur, 32);
+    c->enc1_w = bump(cur, 64 * 288);
+    c->enc1_b = bump(cur, 64);
+    c->enc2_w = bump(cur, 128 * 576);
+    c->enc2_b = bump(cur, 128);
+    c->enc3_w = bump(cur, 128 * 1152);
+    c->enc3_b = bump(cur, 128);
+    prism_adapter_offsets a{};
+    a.in_dim = (int32_t)I;
+    a.up_w = bump(cur, D * I);
+    a.up_b = bump(cur, D);
+    a.down_w = bump(cur, I * D);
+    a.down_b = bump(cur, I);
+    if (ad) *ad = a;
+    c->dec3_w = bump(cur, 128 * 256);
+    c->dec3_b = bump(cur, 128);
+    c->dec2_w = bump(cur, 64 * 192);
+    c->dec2_b = bump(cur, 64);
+    c->dec1_w = bump(cur, 32 * 96);
+    c->dec1_b = bump(cur, 32);
+    c->out_w = bump(cur, 12 * 32);
+    c->out_b = bump(cur, 12);
+    if (end) *end = cur;
+    return PRISM_OK;
+}
+
 extern "C" int prism_validate(const prism_model_desc* desc, const prism_block_offsets* offs,
                               int64_t blob_elems) {
     std::string why;

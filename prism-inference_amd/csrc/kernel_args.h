@@ -87,4 +87,29 @@ typedef struct ProjArgs {
     int64_t n_tokens;
 } ProjArgs;
 
+/* Encoder / decoder stages (codec.hpp). Grid: x = ceil(out pixels /
+ * (64 * CODEC_TT_<stage>)), y = frames; 256 threads. */
+typedef struct CodecArgs {
+    const uint16_t* in;   /* the CHW frame (enc0), an NHWC map, or the decoder's coarse map */
+    const uint16_t* skip; /* decoder skip map (NHWC), NULL for the encoder */
+    uint16_t* out;        /* NHWC output map; the CHW display image for dec1_out */
+    const uint16_t* w;    /* packed [COUT/16][K/32] fragments                 */
+    const float* b;       /* [COUT]                                           */
+    const uint16_t* w2;   /* dec1_out: packed 32 -> 12 fragment, rows padded to 16,
+                             columns permuted to the accumulator lane order    */
+    const float* b2;      /* dec1_out: [16], entries 12..15 zero              */
+    int64_t in_frame, skip_frame, out_frame; /* elements per frame           */
+    int32_t in_w, in_h;   /* conv input map, or the decoder's coarse map      */
+    int32_t out_w, out_h; /* output map (dec1_out: before the PixelShuffle)   */
+} CodecArgs;
+
+/* 16-pixel tiles per wave of each codec stage */
+#define CODEC_TT_ENC0 4
+#define CODEC_TT_ENC1 4
+#define CODEC_TT_ENC2 1
+#define CODEC_TT_ENC3 1
+#define CODEC_TT_DEC3 2
+#define CODEC_TT_DEC2 4
+#define CODEC_TT_DEC1 4
+
 #endif

@@ -1,0 +1,265 @@
+/*
+ * codec.hpp - the conv encoder and fused decoder around the transformer
+ * (the end-to-end frame of vulkan_engine/prism_moe_bench.cpp:387-466).
+ *
+ * Every stage is one implicit GEMM on fp16 MFMA, C^T = W * P^T: the packed
+ * weights are the A operand (16 output channels x 32 k per fragment) and the
+ * B operand is gathered per lane straight from the input maps, 16 output
+ * pixels per token tile. Accumulators start at the bias; the result is
+ * rounded to fp16 once (the reference rounds each 288-wide split partial
+ * sum, strided_conv_split_*ch.comp.glsl:84-93, which its comments call the
+ * same output), then ReLU. Maps between stages are NHWC fp16 (a pixel's
+ * channels contiguous, so a lane's 8 channels are one 16-byte load); the
+ * frame coming in and the display image going out are CHW, as in the
+ * reference.
+ *
+ *   enc0  conv3x3 s1  9 -> 32  + ReLU  conv3x3_coopvec_9ch.comp.glsl:27-72
+ *         (reads the CHW frame; k = ic*9 + tap as the reference, 81 -> 96)
+ *   enc1  conv3x3 s2 32 -> 64  + ReLU  strided_conv_coopvec_32ch.comp.glsl:30-77
+ *   enc2  conv3x3 s2 64 -> 128 + ReLU  strided_conv_split_64ch.comp.glsl:30-93
+ *   enc3  conv3x3 s2 128-> 128 + ReLU  strided_conv_split_128ch.comp.glsl:32-94
+ *         (NHWC taps: k = tap*Cin + ic; the host permutes the weight columns)
+ *   dec3  NN-up(128) ++ skip e2(128) -> PW 256 -> 128 + ReLU   dec3_fused.comp.glsl:27-63
+ *   dec2  NN-up(128) ++ skip e1(64)  -> PW 192 -> 64  + ReLU   dec2_fused.comp.glsl:27-55
+ *   dec1  NN-up(64)  ++ skip e0(32)  -> PW 96  -> 32  + ReLU   dec1_fused.comp.glsl:27-55
+ *         then PW 32 -> 12 (pw_conv_coopvec_32to12.comp.glsl:28-55) and
+ *         PixelShuffle(2) + sigmoid (pixelshuffle_sigmoid.comp.glsl:28-56)
+ *         in the same kernel: dec1's accumulator lanes hold channels
+ *         4g..4g+3 and 16+4g..16+4g+3 of their pixel, which is a B fragment
+ *         of the 32 -> 12 GEMM under the permuted k numbering
+ *         k(g, j) = 16*(j/4) + 4g + j%4 (the host packs that weight with its
+ *         columns permuted to match). The 12 channels round to fp16 (the
+ *         reference's out12 map), then sigmoid in fp32, fp16 again, written
+ *         as 2x2 display pixels of the lane's RGB plane.
+ *
+ * Workgroup = 4 waves; wave w takes TT consecutive 16-pixel tiles (pixels in
+ * row-major order of the output map, blockIdx.y = frame) and all COUT output
+ * channels. Each k-step's weight fragments and B fragments are loaded one
+ * k-step ahead of its MFMAs. Loads at padded or out-of-map positions read a
+ * clamped in-map address and are replaced by zeros.
+ */
+#pragma once
+#include "common.hpp"
+
+/* Output pixel of one lane in one token tile. */
+struct CodecPix {
+    int y, x;
+    bool valid;
+};
+
+/* conv3x3 (pad 1) over an NHWC map with CIN channels; k = tap*CIN + ic. */
+template <int CIN, int STRIDE>
+struct SrcConvNHWC {
+    static constexpr int KS = 9 * CIN / 32;
+    const uint16_t* in;
+    int iw, ih;
+    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
+        constexpr int CPT = CIN / 32; /* k-steps per tap */
+        const int tap = ks / CPT, c0 = (ks % CPT) * 32 + 8 * g;
+        const int iy = p.y * STRIDE + tap / 3 - 1, ix = p.x * STRIDE + tap % 3 - 1;
+        const bool ok = p.valid && iy >= 0 && iy < ih && ix >= 0 && ix < iw;
+        const int64_t pix = ok ? (int64_t)iy * iw + ix : 0;
+        const h8 v = *reinterpret_cast<const h8*>(in + pix * CIN + c0);
+        return ok ? v : h8{};
+    }
+};
+
+/* conv3x3 (pad 1, stride 1) over a CHW frame with 9 channels; k = ic*9 + tap
+ * (the reference's im2col order), 81 real columns padded to 96. */
+struct SrcConvCHW9 {
+    static constexpr int KS = 3;
+    const uint16_t* in;
+    int iw, ih;
+    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
+        h8 v;
+        const int64_t plane = (int64_t)iw * ih;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = 32 * ks + 8 * g + j;
+            const int ic = k / 9, tap = k - 9 * ic;
+            const int iy = p.y + tap / 3 - 1, ix = p.x + tap % 3 - 1;
+            const bool ok = p.valid && k < 81 && iy >= 0 && iy < ih && ix >= 0 && ix < iw;
+            const int64_t off = ok ? ic * plane + (int64_t)iy * iw + ix : 0;
+            const _Float16 e = reinterpret_cast<const _Float16*>(in)[off];
+            v[j] = ok ? e : (_Float16)0.f;
+        }
+        return v;
+    }
+};
+
+/* Decoder input: channels [0, CUP) from the NN-upsampled coarse map (pixel
+ * (min(y/2, uh-1), min(x/2, uw-1))), then [CUP, CUP+CSKIP) from the skip map
+ * at the same pixel. */
+template <int CUP, int CSKIP>
+struct SrcDec {
+    static constexpr int KS = (CUP + CSKIP) / 32;
+    const uint16_t* up;
+    const uint16_t* skip;
+    int uw, uh, ow;
+    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
+        const int y = p.valid ? p.y : 0, x = p.valid ? p.x : 0;
+        h8 v;
+        if (32 * ks < CUP) {
+            const int uy = min(y >> 1, uh - 1), ux = min(x >> 1, uw - 1);
+            v = *reinterpret_cast<const h8*>(up + ((int64_t)uy * uw + ux) * CUP + 32 * ks + 8 * g);
+        } else {
+            v = *reinterpret_cast<const h8*>(skip + ((int64_t)y * ow + x) * CSKIP + 32 * ks - CUP + 8 * g);
+        }
+        return p.valid ? v : h8{};
+    }
+};
+
+/* The GEMM: acc[rt][t] = bias + W[16rt.., :] * P[:, tile t]. */
+template <class Src, int COUT, int TT>
+__device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, const float* bias, const CodecPix (&px)[TT],
+                                           int g, int lane, f4 (&acc)[(COUT + 15) / 16][TT]) {
+    constexpr int RT = (COUT + 15) / 16;
+    constexpr int KS = Src::KS;
+    const FragSrc wsrc(w, (unsigned)(RT * KS * 1024));
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int ch = 16 * r + 4 * g;
+        const f4 bb = {bias[ch], bias[ch + 1], bias[ch + 2], bias[ch + 3]};
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+    }
+    h8 bc[TT], bn[TT], wc[RT], wn[RT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) bc[t] = src.load(0, px[t], g);
+#pragma unroll
+    for (int r = 0; r < RT; ++r) wc[r] = wsrc.load(r * KS, lane * 16);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) bn[t] = src.load(ks + 1, px[t], g);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) wn[r] = wsrc.load(r * KS + ks + 1, lane * 16);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wc[r], bc[t], acc[r][t]);
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) bc[t] = bn[t];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) wc[r] = wn[r];
+        }
+        sched_fence();
+    }
+}
+
+template <int TT>
+__device__ __forceinline__ void codec_pixels(const CodecArgs& a, int wave, int l16, CodecPix (&px)[TT]) {
+    const int npix = a.out_w * a.out_h;
+    const int p0 = (blockIdx.x * 4 + wave) * TT * 16;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int p = p0 + 16 * t + l16;
+        px[t].valid = p < npix;
+        const int q = px[t].valid ? p : 0;
+        px[t].y = q / a.out_w;
+        px[t].x = q - px[t].y * a.out_w;
+    }
+}
+
+/* One stage: GEMM, ReLU, fp16, NHWC store. */
+template <class Src, int COUT, int TT>
+__device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) {
+    constexpr int RT = COUT / 16;
+    static_assert(COUT % 16 == 0, "whole row tiles");
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    CodecPix px[TT];
+    codec_pixels<TT>(a, wave, l16, px);
+    f4 acc[RT][TT];
+    codec_gemm<Src, COUT, TT>(src, a.w, a.b, px, g, lane, acc);
+    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if (!px[t].valid) continue;
+        uint16_t* row = out + ((int64_t)px[t].y * a.out_w + px[t].x) * COUT + 4 * g;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            f4 v = acc[r][t];
+            /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(row + 16 * r) = cvt_h4(v);
+        }
+    }
+}
+
+/* dec1 + output conv + PixelShuffle(2) + sigmoid. */
+template <int TT>
+__device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    CodecPix px[TT];
+    codec_pixels<TT>(a, wave, l16, px);
+    const int f = blockIdx.y;
+    const SrcDec<64, 32> src{a.in + (int64_t)f * a.in_frame, a.skip + (int64_t)f * a.skip_frame, a.in_w, a.in_h,
+                             a.out_w};
+    f4 acc[2][TT];
+    codec_gemm<SrcDec<64, 32>, 32, TT>(src, a.w, a.b, px, g, lane, acc);
+    /* the 32 -> 12 weights: one fragment (rows 12..15 zero), columns permuted */
+    const h8 wo = FragSrc(a.w2, 1024u).load(0, lane * 16);
+    const f4 bo = {a.b2[4 * g], a.b2[4 * g + 1], a.b2[4 * g + 2], a.b2[4 * g + 3]};
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int dw = 2 * a.out_w, dh = 2 * a.out_h;
+    uint16_t* disp = a.out + (int64_t)f * a.out_frame;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        h4 y[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            f4 v = acc[r][t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            y[r] = cvt_h4(v); /* dec1 output, r16 + ReLU */
+        }
+        const h8 yb = {y[0][0], y[0][1], y[0][2], y[0][3], y[1][0], y[1][1], y[1][2], y[1][3]};
+        const h4 o12 = cvt_h4(mfma_16x16x32(wo, yb, bo)); /* out12 channels 4g..4g+3 */
+        if (!px[t].valid || g == 3) continue;             /* rows 12..15 are padding */
+        h4 s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = (float)o12[i];
+            s[i] = (_Float16)fast_rcp(1.0f + fast_exp2(-v * LOG2E));
+        }
+        /* channel 4g + 2sy + sx -> RGB plane g, display pixel (2y + sy, 2x + sx) */
+        uint16_t* base = disp + ((int64_t)g * dh + 2 * px[t].y) * dw + 2 * px[t].x;
+        const uint32_t top = __builtin_bit_cast(uint32_t, __builtin_shufflevector(s, s, 0, 1));
+        const uint32_t bot = __builtin_bit_cast(uint32_t, __builtin_shufflevector(s, s, 2, 3));
+        *reinterpret_cast<uint32_t*>(base) = top;
+        *reinterpret_cast<uint32_t*>(base + dw) = bot;
+    }
+}
+
+#define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))
+
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) {
+    codec_stage<SrcConvCHW9, 32, CODEC_TT_ENC0>(a, SrcConvCHW9{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
+    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc2(CodecArgs a) {
+    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc3(CodecArgs a) {
+    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_dec3(CodecArgs a) {
+    codec_stage<SrcDec<128, 128>, 128, CODEC_TT_DEC3>(
+        a, SrcDec<128, 128>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_dec2(CodecArgs a) {
+    codec_stage<SrcDec<128, 64>, 64, CODEC_TT_DEC2>(
+        a, SrcDec<128, 64>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
+}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_dec1_out(CodecArgs a) { codec_dec_out<CODEC_TT_DEC1>(a); }
+#undef CODEC_FRAME

@@ -8,12 +8,15 @@
  *   prism_router_d{256,128}_n{1..4}                router + counting sort
  *   prism_expert_d{256,128}_bm64                   grouped expert FFN
  *   prism_project_{up,down}_d{256,128}             projection adapters (128 <-> dim)
+ *   prism_codec_enc{0..3}, prism_codec_dec{3,2}    conv encoder / fused decoder stages
+ *   prism_codec_dec1_out                           dec1 + output conv + PixelShuffle + sigmoid
  *   prism_zero_i32                                 clears routing counters
  */
 #include "attn.hpp"
 #include "router.hpp"
 #include "expert.hpp"
 #include "project.hpp"
+#include "codec.hpp"
 
 /* Routing counters must start at zero; a kernel (not a memset node) keeps
  * the launch safe under stream capture. */

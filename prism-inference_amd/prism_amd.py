@@ -88,6 +88,18 @@ class AdapterOffsets(C.Structure):
                 ("down_w", C.c_int64), ("down_b", C.c_int64)]
 
 
+CODEC_FIELDS = ("enc0_w", "enc0_b", "enc1_w", "enc1_b", "enc2_w", "enc2_b", "enc3_w", "enc3_b",
+                "dec3_w", "dec3_b", "dec2_w", "dec2_b", "dec1_w", "dec1_b", "out_w", "out_b")
+# (rows, columns) of each codec weight, in the reference's layouts
+CODEC_SHAPES = {"enc0": (32, 81), "enc1": (64, 288), "enc2": (128, 576), "enc3": (128, 1152),
+                "dec3": (128, 256), "dec2": (64, 192), "dec1": (32, 96), "out": (12, 32)}
+
+
+class CodecOffsets(C.Structure):
+    _fields_ = [("render_w", C.c_int32), ("render_h", C.c_int32), ("in_channels", C.c_int32),
+                ("scale", C.c_int32)] + [(f, C.c_int64) for f in CODEC_FIELDS]
+
+
 class ProjectPush(C.Structure):
     _fields_ = [("n_tokens", C.c_int32), ("pad_", C.c_int32), ("w_offset", C.c_int64),
                 ("b_offset", C.c_int64), ("input_offset", C.c_int64), ("output_offset", C.c_int64)]
@@ -130,6 +142,14 @@ SIGNATURES = {
     "prism_infer_gpu": (C.c_int, [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_int32, C.POINTER(C.c_float)]),
     "prism_import_external_memory": (C.c_int, [_P, C.c_int32, C.c_uint64, C.POINTER(_P), C.POINTER(_P)]),
     "prism_release_external_memory": (C.c_int, [_P, _P]),
+    "prism_codec_layout": (C.c_int, [C.POINTER(ModelDesc), C.c_int32, C.c_int32, C.c_int64, C.POINTER(CodecOffsets),
+                                     C.POINTER(AdapterOffsets), C.POINTER(C.c_int64)]),
+    "prism_load_codec": (C.c_int, [_P, _P, C.c_size_t, C.POINTER(CodecOffsets)]),
+    "prism_encode": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_decode": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_codec_stage": (C.c_int, [_P, C.c_int32, _P, _P, _P, C.c_int32, _P]),
+    "prism_forward_e2e": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_forward_e2e_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
 }
 
 _lib = None
@@ -267,6 +287,44 @@ def synth_adapters(desc: ModelDesc, seed: int = 0, in_dim: int = ADAPTER_IN, std
     for k, (off, n) in enumerate(((a.up_w, D * in_dim), (a.up_b, D), (a.down_w, in_dim * D), (a.down_b, in_dim))):
         blob[off:off + n] = synth_normal(n, seed=seed, stream=(0xAD << 24) | k, std=std)
     return blob, a
+
+
+RENDER = (960, 540)  # the reference's render resolution r0 (prism_moe_bench.cpp:359)
+
+
+def codec_resolutions(render_w: int = RENDER[0], render_h: int = RENDER[1]):
+    """[(w, h)] of r0..r3: each stride-2 conv gives ceil(r / 2)."""
+    r = [(render_w, render_h)]
+    for _ in range(3):
+        w, h = r[-1]
+        r.append(((w + 1) // 2, (h + 1) // 2))
+    return r
+
+
+def codec_layout(desc: ModelDesc, render_w: int = RENDER[0], render_h: int = RENDER[1], base: int = 0):
+    """(CodecOffsets, AdapterOffsets, end): encoder, adapters, decoder from `base`."""
+    c, a, end = CodecOffsets(), AdapterOffsets(), C.c_int64()
+    _check(lib().prism_codec_layout(C.byref(desc), render_w, render_h, base, C.byref(c), C.byref(a), C.byref(end)))
+    return c, a, end.value
+
+
+def synth_codec(desc: ModelDesc, seed: int = 0, render_w: int = RENDER[0], render_h: int = RENDER[1],
+                base: int = 0, adapter_std: float = 0.02):
+    """(blob uint16, CodecOffsets, AdapterOffsets) of the end-to-end section from
+    element `base` on (elements below it are zero): conv / pointwise weights
+    ~N(0, 2/K) for K inputs per output, so activations keep their scale
+    through the ReLU stack; biases ~N(0, 0.02^2); adapters as synth_adapters."""
+    c, a, end = codec_layout(desc, render_w, render_h, base)
+    blob = np.zeros(end, dtype=np.uint16)
+    for k, (name, (rows, cols)) in enumerate(CODEC_SHAPES.items()):
+        wo, bo = getattr(c, name + "_w"), getattr(c, name + "_b")
+        blob[wo:wo + rows * cols] = synth_normal(rows * cols, seed=seed, stream=(0xC0 << 24) | (2 * k),
+                                                 std=float(np.sqrt(2.0 / cols)))
+        blob[bo:bo + rows] = synth_normal(rows, seed=seed, stream=(0xC0 << 24) | (2 * k + 1), std=0.02)
+    D, I = desc.dim, a.in_dim
+    for k, (off, n) in enumerate(((a.up_w, D * I), (a.up_b, D), (a.down_w, I * D), (a.down_b, I))):
+        blob[off:off + n] = synth_normal(n, seed=seed, stream=(0xAD << 24) | k, std=adapter_std)
+    return blob, c, a
 
 
 def read_model_json(path: str):
@@ -466,6 +524,24 @@ class Engine:
 
     def release_external_memory(self, buf):
         _check(self.L.prism_release_external_memory(self.h, buf), self.h)
+
+    def load_codec(self, blob: np.ndarray, coffs: CodecOffsets):
+        blob = np.ascontiguousarray(blob, dtype=np.uint16)
+        _check(self.L.prism_load_codec(self.h, _ptr(blob), blob.nbytes, C.byref(coffs)), self.h)
+        self.coffs = coffs
+
+    def encode(self, frame: int, bottleneck: int, batch: int, stream: int | None = None):
+        _check(self.L.prism_encode(self.h, frame, bottleneck, batch, stream), self.h)
+
+    def decode(self, bottleneck: int, display: int, batch: int, stream: int | None = None):
+        _check(self.L.prism_decode(self.h, bottleneck, display, batch, stream), self.h)
+
+    def codec_stage(self, stage: int, x: int, skip: int | None, y: int, batch: int, stream: int | None = None):
+        _check(self.L.prism_codec_stage(self.h, stage, x, skip, y, batch, stream), self.h)
+
+    def forward_e2e(self, frame: int, display: int, batch: int, stream: int | None = None, graph: bool = False):
+        f = self.L.prism_forward_e2e_graph if graph else self.L.prism_forward_e2e
+        _check(f(self.h, frame, display, batch, stream), self.h)
 
     def load_model_file(self, weights_path: str, json_path: str | None = None):
         _check(self.L.prism_load_model_file(self.h, weights_path.encode(),
