@@ -72,6 +72,75 @@ def time_stage(hip, launch, reps, stream):
     return hip.elapsed_ms(e0, e1) / reps
 
 
+def time_e2e(hip, eng, frame, display, steps, warmup, stream):
+    """ms per end-to-end frame (batch 1), hipGraph replay, HIP events on the stream."""
+    for _ in range(warmup):
+        eng.forward_e2e(frame, display, 1, stream, graph=True)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        eng.forward_e2e(frame, display, 1, stream, graph=True)
+    hip.record(e1, stream)
+    return hip.elapsed_ms(e0, e1) / steps
+
+
+# Encoder / decoder stages: (name, input channels at its input resolution,
+# skip channels, output channels, input res index, output res index, MACs per
+# output pixel). dec1's output is the 12-channel render-resolution map that its
+# kernel shuffles to the display (3 x 2x2 per pixel); its MACs include the
+# 32 -> 12 output conv.
+CODEC_STAGES = [("enc0", 9, 0, 32, 0, 0, 32 * 81), ("enc1", 32, 0, 64, 0, 1, 64 * 288),
+                ("enc2", 64, 0, 128, 1, 2, 128 * 576), ("enc3", 128, 0, 128, 2, 3, 128 * 1152),
+                ("dec3", 128, 128, 128, 3, 2, 128 * 256), ("dec2", 128, 64, 64, 2, 1, 64 * 192),
+                ("dec1_out", 64, 32, 12, 1, 0, 32 * 96 + 12 * 32)]
+
+
+def codec_section(hip, eng, desc, steps, warmup, reps, stream):
+    """The end-to-end frame at batch 1 and each codec stage's duration, with
+    its algorithmic HBM bytes (input map + skip map + output map + weights,
+    each once) against the 8 TB/s peak."""
+    cblob, coffs, _ = P.synth_codec(desc, seed=3)
+    eng.load_codec(cblob, coffs)
+    r = P.codec_resolutions()
+    pix = [w * h for w, h in r]
+    w0, h0 = r[0]
+    frame, disp = hip.malloc(9 * pix[0] * 2), hip.malloc(12 * pix[0] * 2)
+    hip.upload(frame, P.synth_normal(9 * pix[0], seed=4))
+    ms_e2e = time_e2e(hip, eng, frame, disp, steps, warmup, stream)
+    # per stage, on maps the encoder just wrote (so every input is realistic)
+    bufs = {}
+    for name, cin, cskip, cout, ri, ro, macs in CODEC_STAGES:
+        bufs[name] = hip.malloc(pix[ro] * cout * 2)
+    b3 = hip.malloc(pix[3] * 128 * 2)
+    eng.encode(frame, b3, 1)
+    hip.sync()
+    src = {"enc0": (frame, None), "enc1": (bufs["enc0"], None), "enc2": (bufs["enc1"], None),
+           "enc3": (bufs["enc2"], None), "dec3": (b3, bufs["enc2"]), "dec2": (bufs["dec3"], bufs["enc1"]),
+           "dec1_out": (bufs["dec2"], bufs["enc0"])}
+    stages = {}
+    wbytes_all = 0
+    for st, (name, cin, cskip, cout, ri, ro, macs) in enumerate(CODEC_STAGES):
+        x, skip = src[name]
+        y = bufs[name]
+        ms = time_stage(hip, lambda: eng.L.prism_codec_stage(eng.h, st, x, skip, y, 1, stream), reps, stream)
+        wbytes = macs * 2
+        wbytes_all += wbytes
+        nbytes = pix[ri] * cin * 2 + pix[ro] * (cskip + cout) * 2 + wbytes
+        stages[name] = {"ms": round(ms, 5), "bytes": int(nbytes), "hbm_frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
+                        "tflops": round(2 * macs * pix[ro] / (ms * 1e-3) / 1e12, 2)}
+    total = sum(v["ms"] for v in stages.values())
+    for ptr in list(bufs.values()) + [frame, disp, b3]:
+        hip.free(ptr)
+    return {"frame_ms": round(ms_e2e, 5), "frames_per_s": round(1e3 / ms_e2e, 2),
+            "codec_ms": round(total, 5),
+            "codec_hbm_frac": round(sum(v["bytes"] for v in stages.values()) / (total * 1e-3) / HBM_PEAK, 4),
+            "stages": stages,
+            "workload": f"render {w0}x{h0} (9-channel frame) -> encoder -> proj 128->256 -> 16 MoE-64 blocks at "
+                        f"{r[3][0]}x{r[3][1]} -> proj 256->128 -> decoder -> 3x{2 * w0}x{2 * h0} display, batch 1, "
+                        "hipGraph replay; codec weights ~N(0, 2/K)"}
+
+
 def measured_traffic(kernel, grid):
     """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (calibrated against a device copy of known size), if it covers this
@@ -209,6 +278,8 @@ def main():
                 "note": "pw_project 128->256 (+ReLU) and 256->128 around the 16 blocks, batch " + str(B)}
     for ptr in (proj, ax, ay):
         hip.free(ptr)
+    log("[bench] end-to-end frame and codec stages")
+    e2e = codec_section(hip, eng, desc, max(20, args.steps // 2), 5, args.stage_reps, stream)
 
     # ---- expert load actually produced (all blocks, batch B)
     share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
@@ -250,6 +321,7 @@ def main():
                         "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},
         "wall_s_timed": round(wall_b, 3),
         "adapters": adapters,
+        "e2e_frame": e2e,
     }
     hip.free(feats)
     hip.free(aux)

@@ -285,7 +285,7 @@ int prism_load_model_file(prism_ctx* ctx, const char* weights_path, const char* 
 
 /* ---- conv encoder / fused decoder (the end-to-end frame) ---------------- */
 
-/* The end-to-end frame of prism_moe_bench.cpp:387-466 around the blocks:
+/* The end-to-end frame of prism_moe_bench.cpp:387-471 around the blocks:
  *   encoder  enc0 conv3x3 9->32 (render resolution r0), enc1 conv3x3/2 32->64
  *            (r1), enc2 conv3x3/2 64->128 (r2), enc3 conv3x3/2 128->128 (r3 =
  *            the token grid), each + ReLU;

@@ -1,7 +1,7 @@
 /*
  * codec.cpp - host side of the conv encoder / fused decoder (kernels in
  * csrc/kernels/codec.hpp): weight repacking, the codec workspace and the
- * stage launches of the end-to-end frame (prism_moe_bench.cpp:387-466).
+ * stage launches of the end-to-end frame (prism_moe_bench.cpp:387-471).
  *
  * Weights arrive in the reference's layouts (row-major [out][in]; conv
  * columns k = ic*9 + ky*3 + kx) and are repacked once into MFMA A-fragment

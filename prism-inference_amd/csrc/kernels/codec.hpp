@@ -1,6 +1,6 @@
 /*
  * codec.hpp - the conv encoder and fused decoder around the transformer
- * (the end-to-end frame of vulkan_engine/prism_moe_bench.cpp:387-466).
+ * (the end-to-end frame of vulkan_engine/prism_moe_bench.cpp:387-471).
  *
  * Every stage is one implicit GEMM on fp16 MFMA, C^T = W * P^T: the packed
  * weights are the A operand (16 output channels x 32 k per fragment) and the
