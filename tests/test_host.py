@@ -264,3 +264,26 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_codec_layout_follows_the_reference_order():
+    """enc_ic, enc1, enc2, enc3, proj_up, proj_dn, d3, d2, d1, out
+    (prism_moe_bench.cpp:347-357), 8-aligned, after the blocks."""
+    desc = P.CONFIGS["moe64"].desc()
+    _, total = P.layout(desc)
+    c, a, end = P.codec_layout(desc, 960, 540, base=total)
+    D = desc.dim
+    order = [(c.enc0_w, 32 * 81), (c.enc0_b, 32), (c.enc1_w, 64 * 288), (c.enc1_b, 64), (c.enc2_w, 128 * 576),
+             (c.enc2_b, 128), (c.enc3_w, 128 * 1152), (c.enc3_b, 128), (a.up_w, D * 128), (a.up_b, D),
+             (a.down_w, 128 * D), (a.down_b, 128), (c.dec3_w, 128 * 256), (c.dec3_b, 128), (c.dec2_w, 64 * 192),
+             (c.dec2_b, 64), (c.dec1_w, 32 * 96), (c.dec1_b, 32), (c.out_w, 12 * 32), (c.out_b, 12)]
+    assert order[0][0] == (total + 7) // 8 * 8
+    for (o, n), (o2, _) in zip(order, order[1:]):
+        assert o % 8 == 0 and o2 == o + (n + 7) // 8 * 8
+    assert end == order[-1][0] + 12
+    assert (c.render_w, c.render_h, c.in_channels, c.scale) == (960, 540, 9, 2)
+    assert P.codec_resolutions(960, 540) == [(960, 540), (480, 270), (240, 135), (120, 68)]
+    # a render size that does not encode to the 120x68 token grid
+    with pytest.raises(P.PrismError) as ei:
+        P.codec_layout(desc, 960, 530)
+    assert ei.value.code == P.ERR_INVALID and "encodes to" in P.lib().prism_last_error(None).decode()
