@@ -5,7 +5,9 @@
  * :25-33, zero-vector padded slots :31-37, QKV :39-51, softmax core :53-69,
  * out-proj + fp16 residual :71-78) with the pre-LayerNorm added, as:
  *
- *  1. LN1 of the window's 64 slots -> xs (LDS, fp16). Padded slots are zero.
+ *  1. LN1 of the window's 64 slots -> xs (LDS, fp16), the raw rows -> os
+ *     (they are the residual; the out-proj's epilogue reads them from there,
+ *     so x is fetched from HBM once). Padded slots are zero.
  *  2. Wave w owns heads w and w+4 (8-wave variant: head w). Per head, one
  *     MFMA GEMM pass over the model dim produces Q^T and K^T (rows = channel,
  *     cols = token) and V
@@ -16,10 +18,12 @@
  *     k(g, j) = 16*(j/4) + 4g + j%4. Softmax runs down the key axis: 16
  *     values in-lane plus two cross-lane xor shuffles. P = exp(...) stays in
  *     registers and O^T = V^T P^T is again register-to-register MFMA.
- *     O^T is normalised, rounded to fp16 and written to os (LDS).
- *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x (fp16 round), store.
- *  5. Routed variants (NPT > 0, the block chain's MoE blocks) keep the output
- *     tile in LDS and route it there: waves 0-3 each take 16 tokens through
+ *     O^T is normalised, rounded to fp16 and kept in registers until every
+ *     wave has finished reading xs; then all heads' O^T go to xs.
+ *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x from os (fp16 round),
+ *     store; the result also overwrites the lane's residual in os.
+ *  5. Routed variants (NPT > 0, the block chain's MoE blocks) route that
+ *     output tile from os: waves 0-3 each take 16 tokens through
  *     LN2 + router GEMM + argmax (route_token, whose W_r fragments continue
  *     the weight ring), then the window's counting sort (LDS histogram, one
  *     global atomic per present expert, bucket scatter). This replaces the
@@ -173,13 +177,16 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
         for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
     __syncthreads(); /* parameters staged */
 #pragma unroll
-    for (int it = 0; it < IT; ++it)
-        ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + (wave * SPW + it * SPI + lane / LPS) * LDS, nullptr);
+    for (int it = 0; it < IT; ++it) {
+        const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+        ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + row, os + row); /* os: the raw rows (residual) */
+    }
     __syncthreads();
 
     /* ---- 2./3. per head ----------------------------------------------- */
     static_assert(S::HEADF % PF == 0, "ring slots must not depend on the head index");
-#pragma unroll 1
+    h4 okeep[S::HPW][CT][4]; /* O^T of each head (channel tile, query tile) until xs is free */
+#pragma unroll
     for (int hh = 0; hh < S::HPW; ++hh) {
         /* keeps the head-invariant xs reads inside the loop (hoisting all of
          * them out would pin 32 fragments in registers) */
@@ -302,28 +309,23 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                                    p[2 * st + 1][qt][3]};
                     o = mfma_16x16x32(va, pb, o);
                 }
-                const h4 r = cvt_h4(o * inv[qt]);
-                *reinterpret_cast<h4*>(os + (16 * qt + l16) * LDS + h * HD + 16 * dt + 4 * g) = r;
+                okeep[hh][dt][qt] = cvt_h4(o * inv[qt]);
             }
     }
 
-    /* residual rows for the epilogue, fetched while the out-proj runs */
-    h4 xin[4][ORT];
-    bool vt[4];
-    int64_t tbase[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int s = 16 * t + l16;
-        const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-        vt[t] = gy < a.H && gx < a.W;
-        tbase[t] = (int64_t)(vt[t] ? gy * a.W + gx : 0) * DIM;
-#pragma unroll
-        for (int r = 0; r < ORT; ++r)
-            xin[t][r] = *reinterpret_cast<const h4*>(in + tbase[t] + (wave * ORT + r) * 16 + 4 * g);
-    }
+    /* every wave has read xs for the last time: O of all heads goes there */
     __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < S::HPW; ++hh)
+#pragma unroll
+        for (int dt = 0; dt < CT; ++dt)
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt)
+                *reinterpret_cast<h4*>(xs + (16 * qt + l16) * LDS + (wave + NW * hh) * HD + 16 * dt + 4 * g) =
+                    okeep[hh][dt][qt];
     if constexpr (NPT > 0) /* the QKV biases are dead now */
         if (threadIdx.x < 64) r_hist[threadIdx.x] = 0;
+    __syncthreads();
 
     /* ---- 4. out-proj + residual --------------------------------------- */
     f4 acc[ORT][4]; /* starts at the out-proj bias */
@@ -336,13 +338,13 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     }
     h8 of[4], on[4]; /* double-buffered like the QKV operands */
 #pragma unroll
-    for (int t = 0; t < 4; ++t) of[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 8 * g);
+    for (int t = 0; t < 4; ++t) of[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                on[t] = *reinterpret_cast<const h8*>(os + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+                on[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
         }
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
@@ -361,26 +363,31 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+        const int sl = 16 * t + l16;
+        const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
+        const bool vt = gy < a.H && gx < a.W;
+        uint16_t* orow = out + (int64_t)(vt ? gy * a.W + gx : 0) * DIM;
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
             const int ch = (wave * ORT + r) * 16 + 4 * g;
+            h4* xr = reinterpret_cast<h4*>(os + sl * LDS + ch); /* this lane's residual, read once */
             /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding) */
-            const h4 y = add_f16x4(cvt_h4(acc[r][t]), xin[t][r]);
-            if (vt[t]) *reinterpret_cast<h4*>(out + tbase[t] + ch) = y;
-            /* the tile stays on chip for routing; xs is free since the head loop */
-            if constexpr (NPT > 0) *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = y;
+            const h4 y = add_f16x4(cvt_h4(acc[r][t]), *xr);
+            if (vt) *reinterpret_cast<h4*>(orow + ch) = y;
+            /* the tile stays on chip for routing, over its residual */
+            if constexpr (NPT > 0) *xr = y;
         }
     }
 
     /* ---- 5. fused routing (moe_router.comp.glsl:24-52 + counting sort) -- */
     if constexpr (NPT > 0) {
-        __syncthreads(); /* y tile complete in xs */
+        __syncthreads(); /* y tile complete in os */
         if (routes) {    /* wave w: tokens 16w..16w+15, all experts */
             const int sl = 16 * wave + l16;
             const int sy = wy * 8 + (sl >> 3), sx = wxx * 8 + (sl & 7);
             h8 cur[KS];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(xs + sl * LDS + 32 * ks + 8 * g);
+            for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
             const int e = route_token<DIM, NPT>(cur, s_g2, s_b2, s_br, g, a.n_experts, [&](int rt, int ks) {
                 const int p = S::RBASE + ks * NPT + rt;
                 const h8 w = ring[p % PF];
