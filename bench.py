@@ -315,7 +315,7 @@ def main():
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "traffic_source": traffic_src,
                      "flops_per_launch": route_flops, "avg_launch_ms": round(t_route, 5),
-                     "timed": "prism_attn_route stage call: the routed attention kernel + its 1-workgroup counter clear"},
+                     "timed": "prism_attn_route stage call: the routed attention kernel + its 1-workgroup count copy"},
         "expert_load": {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
                         "hottest_share_mean": round(float(share.mean()), 4),
                         "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},

@@ -191,7 +191,10 @@ int prism_experts(prism_ctx* ctx, const prism_expert_push* p, void* features,
  * features at pa->output_offset, assignment, counts and perm come out as
  * prism_attn followed by prism_router would leave them (bit-identical expert
  * ids and counts; the order inside a bucket is unspecified). No reference
- * counterpart as a single call: the block chain uses it for MoE blocks. */
+ * counterpart as a single call: the block chain uses it for MoE blocks. The
+ * kernel counts into a row of the context's own, counters 256 bytes apart,
+ * and a one-workgroup launch copies the totals to `counts`: calls on one
+ * context must not overlap on different streams. */
 int prism_attn_route(prism_ctx* ctx, const prism_attn_push* pa, const prism_router_push* pr,
                      void* features, int32_t* aux, int32_t batch, void* stream);
 

@@ -54,6 +54,7 @@ struct prism_ctx {
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
     hipFunction_t f_zero = nullptr;
+    hipFunction_t f_take = nullptr;
     hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */
     hipFunction_t f_codec[7] = {};     /* enc0..enc3, dec3, dec2, dec1_out */
     std::string err;
@@ -82,6 +83,8 @@ struct prism_ctx {
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
+    int32_t* stage_counts = nullptr; /* prism_attn_route: private counters, CHAIN_COUNT_STRIDE apart */
+    bool stage_dirty = false;        /* ... possibly nonzero (a call stopped between its launches) */
 
     hipStream_t user_stream = nullptr;  /* prism_init_with_device: the renderer's stream */
     hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr; /* prism_infer_gpu timing */

@@ -95,7 +95,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
         {&c->f_expert[0][0], "prism_expert_d128_bm64"},  {&c->f_expert[1][0], "prism_expert_d256_bm64"},
         {&c->f_expert[0][1], "prism_expert_d128_bm64_w8"}, {&c->f_expert[1][1], "prism_expert_d256_bm64_w8"},
-        {&c->f_zero, "prism_zero_i32"},
+        {&c->f_zero, "prism_zero_i32"}, {&c->f_take, "prism_take_counts"},
         {&c->f_proj[0][0], "prism_project_up_d128"},   {&c->f_proj[0][1], "prism_project_down_d128"},
         {&c->f_proj[1][0], "prism_project_up_d256"},   {&c->f_proj[1][1], "prism_project_down_d256"},
         {&c->f_codec[0], "prism_codec_enc0"}, {&c->f_codec[1], "prism_codec_enc1"},
@@ -187,6 +187,7 @@ extern "C" void prism_destroy(prism_ctx* c) {
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
     if (c->ev_t0) (void)hipEventDestroy(c->ev_t0);
     if (c->ev_t1) (void)hipEventDestroy(c->ev_t1);
+    if (c->stage_counts) (void)hipFree(c->stage_counts);
     if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
@@ -650,12 +651,34 @@ extern "C" int prism_attn_route(prism_ctx* c, const prism_attn_push* pa, const p
         return fail(c, PRISM_ERR_INVALID, "the router must read the attention output (input_offset %lld != %lld)",
                     (long long)pr->input_offset, (long long)pa->output_offset);
     HIP_TRY(c, hipSetDevice(c->device));
-    rc = enqueue_zero(c, aux + pr->count_offset, pr->n_experts, (hipStream_t)stream);
-    if (rc) return rc;
+    /* The kernel counts into a private row, counters 256 B apart as in the
+     * chain (every workgroup adds to them; adjacent counters would serialise
+     * those atomics), and prism_take_counts moves the totals to the caller's
+     * contiguous counts, clearing the row for the next call. */
+    const hipStream_t s = (hipStream_t)stream;
+    if (!c->stage_counts) {
+        const size_t bytes = sizeof(int32_t) * 64 * CHAIN_COUNT_STRIDE;
+        HIP_TRY(c, hipMalloc((void**)&c->stage_counts, bytes));
+        HIP_TRY(c, hipMemset(c->stage_counts, 0, bytes));
+    }
+    if (c->stage_dirty) {
+        rc = enqueue_zero(c, c->stage_counts, 64 * CHAIN_COUNT_STRIDE, s);
+        if (rc) return rc;
+        c->stage_dirty = false;
+    }
     uint16_t* f = static_cast<uint16_t*>(features);
-    const RouteOut ro{aux + pr->assignment_offset, aux + pr->count_offset, aux + pr->perm_offset, 1, nullptr};
-    return enqueue_attn(c, *ka, f + pa->input_offset, f + pa->output_offset, pa->spatial_h, pa->spatial_w, batch,
-                        (hipStream_t)stream, &ro);
+    const RouteOut ro{aux + pr->assignment_offset, c->stage_counts, aux + pr->perm_offset, CHAIN_COUNT_STRIDE, nullptr};
+    c->stage_dirty = true;
+    rc = enqueue_attn(c, *ka, f + pa->input_offset, f + pa->output_offset, pa->spatial_h, pa->spatial_w, batch, s, &ro);
+    if (rc) return rc;
+    int32_t* src = c->stage_counts;
+    int32_t stride = CHAIN_COUNT_STRIDE, n = pr->n_experts;
+    int32_t* dst = aux + pr->count_offset;
+    void* params[] = {&src, &stride, &dst, &n};
+    const hipError_t e = hipModuleLaunchKernel(c->f_take, 1, 1, 1, 64, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(take counts): %s", hipGetErrorString(e));
+    c->stage_dirty = false;
+    return PRISM_OK;
 }
 
 extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* features, int32_t* aux, int32_t batch,
