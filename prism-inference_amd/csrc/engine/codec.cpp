@@ -24,7 +24,7 @@ using namespace prism;
 namespace {
 
 enum { ST_ENC0, ST_ENC1, ST_ENC2, ST_ENC3, ST_DEC3, ST_DEC2, ST_DEC1, N_STAGES };
-const int kTT[N_STAGES] = {CODEC_TT_ENC0, CODEC_TT_ENC1, CODEC_TT_ENC2, CODEC_TT_ENC3,
+const int kTT[N_STAGES] = {4, CODEC_TT_ENC1, CODEC_TT_ENC2, CODEC_TT_ENC3, /* enc0: own grid */
                            CODEC_TT_DEC3, CODEC_TT_DEC2, CODEC_TT_DEC1};
 const int kInRes[N_STAGES] = {0, 0, 1, 2, 3, 2, 1};  /* resolution index of the (coarse) input map */
 const int kOutRes[N_STAGES] = {0, 1, 2, 3, 2, 1, 0}; /* of the output map (dec1: before the shuffle) */
@@ -57,7 +57,9 @@ int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip,
     a.skip_frame = out_pix * kSkipCh[st];
     a.out_frame = out_pix * kOutCh[st];
     const int64_t per_wg = 64 * kTT[st];
-    const unsigned gx = (unsigned)((out_pix + per_wg - 1) / per_wg);
+    const unsigned gx = st == ST_ENC0 ? (unsigned)(((a.out_w + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS) *
+                                                  ((a.out_h + CODEC_ENC0_ROWS - 1) / CODEC_ENC0_ROWS))
+                                      : (unsigned)((out_pix + per_wg - 1) / per_wg);
     void* params[] = {&a};
     const hipError_t e = hipModuleLaunchKernel(c->f_codec[st], gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(codec stage %d): %s", st, hipGetErrorString(e));

@@ -88,7 +88,8 @@ typedef struct ProjArgs {
 } ProjArgs;
 
 /* Encoder / decoder stages (codec.hpp). Grid: x = ceil(out pixels /
- * (64 * CODEC_TT_<stage>)), y = frames; 256 threads. */
+ * (64 * CODEC_TT_<stage>)) (enc0: blocks of CODEC_ENC0_ROWS x CODEC_ENC0_COLS), y = frames;
+ * 256 threads. */
 typedef struct CodecArgs {
     const uint16_t* in;   /* the CHW frame (enc0), an NHWC map, or the decoder's coarse map */
     const uint16_t* skip; /* decoder skip map (NHWC), NULL for the encoder */
@@ -104,8 +105,10 @@ typedef struct CodecArgs {
 } CodecArgs;
 
 /* 16-pixel tiles per wave of each codec stage */
-#define CODEC_TT_ENC0 4
 #define CODEC_TT_ENC1 4
+/* enc0 output block per workgroup (rows x columns) */
+#define CODEC_ENC0_ROWS 4
+#define CODEC_ENC0_COLS 64
 #define CODEC_TT_ENC2 1
 #define CODEC_TT_ENC3 1
 #define CODEC_TT_DEC3 2

@@ -14,7 +14,8 @@
  * reference.
  *
  *   enc0  conv3x3 s1  9 -> 32  + ReLU  conv3x3_coopvec_9ch.comp.glsl:27-72
- *         (reads the CHW frame; k = ic*9 + tap as the reference, 81 -> 96)
+ *         (reads the CHW frame through an LDS window per 4 x 64 pixel block;
+ *         k = ic*9 + tap as the reference, 81 -> 96)
  *   enc1  conv3x3 s2 32 -> 64  + ReLU  strided_conv_coopvec_32ch.comp.glsl:30-77
  *   enc2  conv3x3 s2 64 -> 128 + ReLU  strided_conv_split_64ch.comp.glsl:30-93
  *   enc3  conv3x3 s2 128-> 128 + ReLU  strided_conv_split_128ch.comp.glsl:32-94
@@ -61,29 +62,6 @@ struct SrcConvNHWC {
         const int64_t pix = ok ? (int64_t)iy * iw + ix : 0;
         const h8 v = *reinterpret_cast<const h8*>(in + pix * CIN + c0);
         return ok ? v : h8{};
-    }
-};
-
-/* conv3x3 (pad 1, stride 1) over a CHW frame with 9 channels; k = ic*9 + tap
- * (the reference's im2col order), 81 real columns padded to 96. */
-struct SrcConvCHW9 {
-    static constexpr int KS = 3;
-    const uint16_t* in;
-    int iw, ih;
-    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
-        h8 v;
-        const int64_t plane = (int64_t)iw * ih;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int k = 32 * ks + 8 * g + j;
-            const int ic = k / 9, tap = k - 9 * ic;
-            const int iy = p.y + tap / 3 - 1, ix = p.x + tap % 3 - 1;
-            const bool ok = p.valid && k < 81 && iy >= 0 && iy < ih && ix >= 0 && ix < iw;
-            const int64_t off = ok ? ic * plane + (int64_t)iy * iw + ix : 0;
-            const _Float16 e = reinterpret_cast<const _Float16*>(in)[off];
-            v[j] = ok ? e : (_Float16)0.f;
-        }
-        return v;
     }
 };
 
@@ -239,11 +217,83 @@ __device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
     }
 }
 
+/* enc0: conv3x3 9 -> 32 + ReLU straight from the CHW frame. A workgroup
+ * takes a block of CODEC_ENC0_ROWS x 64 output pixels (wave w: row w, 4 tiles of 16
+ * columns); the block's 9-channel input window with its 1-pixel halo is
+ * first copied into LDS with coalesced row loads, and each lane then gathers
+ * its B fragment elements (k = ic*9 + tap, the reference's im2col order,
+ * 81 -> 96) from LDS. Grid: x = ceil(W/CODEC_ENC0_COLS) * ceil(H/CODEC_ENC0_ROWS), y = frames. */
+__device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
+    constexpr int IR = CODEC_ENC0_ROWS + 2, IC = CODEC_ENC0_COLS + 2, CH = 9, TT = CODEC_ENC0_COLS / 16;
+    __shared__ f16 s_in[CH * IR * IC];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int W = a.out_w, H = a.out_h;
+    const int bxn = (W + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS;
+    const int by0 = (blockIdx.x / bxn) * CODEC_ENC0_ROWS, bx0 = (blockIdx.x % bxn) * CODEC_ENC0_COLS;
+    const f16* frame = reinterpret_cast<const f16*>(a.in) + (int64_t)blockIdx.y * a.in_frame;
+    const int64_t plane = (int64_t)W * H;
+    for (int i = threadIdx.x; i < CH * IR * IC; i += 256) {
+        const int c = i / (IR * IC), rem = i - c * (IR * IC), r = rem / IC, x = rem - r * IC;
+        const int gy = by0 - 1 + r, gx = bx0 - 1 + x;
+        const bool ok = gy >= 0 && gy < H && gx >= 0 && gx < W;
+        const f16 v = frame[ok ? c * plane + (int64_t)gy * W + gx : 0];
+        s_in[i] = ok ? v : (f16)0.f;
+    }
+    /* this lane's 24 (k-step, element) gather offsets: channel, tap row and column */
+    int off[3][8];
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = 32 * ks + 8 * g + j;
+            const int ic = k / 9, tap = k - 9 * ic;
+            off[ks][j] = k < 81 ? ic * (IR * IC) + (tap / 3) * IC + tap % 3 : -1;
+        }
+    __syncthreads();
+    const FragSrc wsrc(a.w, 2u * 3u * 1024u);
+    f4 acc[2][TT];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int ch = 16 * r + 4 * g;
+        const f4 bb = {a.b[ch], a.b[ch + 1], a.b[ch + 2], a.b[ch + 3]};
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+    }
+    const int base = wave * IC + l16; /* output row `wave`, column 16t + l16 of the block */
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks) {
+        const h8 w0 = wsrc.load(0 * 3 + ks, lane * 16), w1 = wsrc.load(1 * 3 + ks, lane * 16);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            h8 b;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b[j] = off[ks][j] >= 0 ? s_in[off[ks][j] + base + 16 * t] : (f16)0.f;
+            acc[0][t] = mfma_16x16x32(w0, b, acc[0][t]);
+            acc[1][t] = mfma_16x16x32(w1, b, acc[1][t]);
+        }
+    }
+    const int oy = by0 + wave;
+    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int ox = bx0 + 16 * t + l16;
+        if (oy >= H || ox >= W) continue;
+        uint16_t* row = out + ((int64_t)oy * W + ox) * 32 + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            f4 v = acc[r][t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(row + 16 * r) = cvt_h4(v);
+        }
+    }
+}
+
 #define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))
 
-extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) {
-    codec_stage<SrcConvCHW9, 32, CODEC_TT_ENC0>(a, SrcConvCHW9{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
-}
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
     codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
 }
