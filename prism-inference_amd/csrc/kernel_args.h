@@ -104,7 +104,9 @@ typedef struct CodecArgs {
     int32_t out_w, out_h; /* output map (dec1_out: before the PixelShuffle)   */
 } CodecArgs;
 
-/* 16-pixel tiles per wave of each codec stage */
+/* 16-pixel tiles per wave of each codec stage, and (RS) how many waves share a
+ * pixel group, splitting its output channels: a workgroup covers
+ * 16 * TT * 4 / RS pixels */
 #define CODEC_TT_ENC1 4
 /* enc0 output block per workgroup (rows x columns) */
 #define CODEC_ENC0_ROWS 4
@@ -114,5 +116,10 @@ typedef struct CodecArgs {
 #define CODEC_TT_DEC3 2
 #define CODEC_TT_DEC2 4
 #define CODEC_TT_DEC1 4
+#define CODEC_RS_ENC1 1
+#define CODEC_RS_ENC2 1
+#define CODEC_RS_ENC3 4
+#define CODEC_RS_DEC3 1
+#define CODEC_RS_DEC2 1
 
 #endif

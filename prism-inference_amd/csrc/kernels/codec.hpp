@@ -87,16 +87,16 @@ struct SrcDec {
     }
 };
 
-/* The GEMM: acc[rt][t] = bias + W[16rt.., :] * P[:, tile t]. */
-template <class Src, int COUT, int TT>
+/* The GEMM: acc[r][t] = bias + W[16(rt0 + r).., :] * P[:, tile t] for RT row
+ * tiles from rt0 (of the matrix's RTALL). */
+template <class Src, int RTALL, int RT, int TT>
 __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, const float* bias, const CodecPix (&px)[TT],
-                                           int g, int lane, f4 (&acc)[(COUT + 15) / 16][TT]) {
-    constexpr int RT = (COUT + 15) / 16;
+                                           int g, int lane, int rt0, f4 (&acc)[RT][TT]) {
     constexpr int KS = Src::KS;
-    const FragSrc wsrc(w, (unsigned)(RT * KS * 1024));
+    const FragSrc wsrc(w, (unsigned)(RTALL * KS * 1024));
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
-        const int ch = 16 * r + 4 * g;
+        const int ch = 16 * (rt0 + r) + 4 * g;
         const f4 bb = {bias[ch], bias[ch + 1], bias[ch + 2], bias[ch + 3]};
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = bb;
@@ -105,14 +105,14 @@ __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, co
 #pragma unroll
     for (int t = 0; t < TT; ++t) bc[t] = src.load(0, px[t], g);
 #pragma unroll
-    for (int r = 0; r < RT; ++r) wc[r] = wsrc.load(r * KS, lane * 16);
+    for (int r = 0; r < RT; ++r) wc[r] = wsrc.load((rt0 + r) * KS, lane * 16);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) {
 #pragma unroll
             for (int t = 0; t < TT; ++t) bn[t] = src.load(ks + 1, px[t], g);
 #pragma unroll
-            for (int r = 0; r < RT; ++r) wn[r] = wsrc.load(r * KS + ks + 1, lane * 16);
+            for (int r = 0; r < RT; ++r) wn[r] = wsrc.load((rt0 + r) * KS + ks + 1, lane * 16);
         }
 #pragma unroll
         for (int r = 0; r < RT; ++r)
@@ -128,10 +128,12 @@ __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, co
     }
 }
 
-template <int TT>
+/* A workgroup's 4 waves form 4/RS pixel groups of TT tiles each; the RS waves
+ * of a group split the output channels. */
+template <int TT, int RS>
 __device__ __forceinline__ void codec_pixels(const CodecArgs& a, int wave, int l16, CodecPix (&px)[TT]) {
     const int npix = a.out_w * a.out_h;
-    const int p0 = (blockIdx.x * 4 + wave) * TT * 16;
+    const int p0 = (blockIdx.x * (4 / RS) + wave / RS) * TT * 16;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         const int p = p0 + 16 * t + l16;
@@ -143,22 +145,23 @@ __device__ __forceinline__ void codec_pixels(const CodecArgs& a, int wave, int l
 }
 
 /* One stage: GEMM, ReLU, fp16, NHWC store. */
-template <class Src, int COUT, int TT>
+template <class Src, int COUT, int TT, int RS>
 __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) {
-    constexpr int RT = COUT / 16;
-    static_assert(COUT % 16 == 0, "whole row tiles");
+    constexpr int RTALL = COUT / 16, RT = RTALL / RS;
+    static_assert(COUT % 16 == 0 && RTALL % RS == 0 && 4 % RS == 0, "whole row tiles");
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     CodecPix px[TT];
-    codec_pixels<TT>(a, wave, l16, px);
+    codec_pixels<TT, RS>(a, wave, l16, px);
+    const int rt0 = (wave % RS) * RT;
     f4 acc[RT][TT];
-    codec_gemm<Src, COUT, TT>(src, a.w, a.b, px, g, lane, acc);
+    codec_gemm<Src, RTALL, RT, TT>(src, a.w, a.b, px, g, lane, rt0, acc);
     uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         if (!px[t].valid) continue;
-        uint16_t* row = out + ((int64_t)px[t].y * a.out_w + px[t].x) * COUT + 4 * g;
+        uint16_t* row = out + ((int64_t)px[t].y * a.out_w + px[t].x) * COUT + 16 * rt0 + 4 * g;
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f4 v = acc[r][t];
@@ -177,12 +180,12 @@ __device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     CodecPix px[TT];
-    codec_pixels<TT>(a, wave, l16, px);
+    codec_pixels<TT, 1>(a, wave, l16, px);
     const int f = blockIdx.y;
     const SrcDec<64, 32> src{a.in + (int64_t)f * a.in_frame, a.skip + (int64_t)f * a.skip_frame, a.in_w, a.in_h,
                              a.out_w};
     f4 acc[2][TT];
-    codec_gemm<SrcDec<64, 32>, 32, TT>(src, a.w, a.b, px, g, lane, acc);
+    codec_gemm<SrcDec<64, 32>, 2, 2, TT>(src, a.w, a.b, px, g, lane, 0, acc);
     /* the 32 -> 12 weights: one fragment (rows 12..15 zero), columns permuted */
     const h8 wo = FragSrc(a.w2, 1024u).load(0, lane * 16);
     const f4 bo = {a.b2[4 * g], a.b2[4 * g + 1], a.b2[4 * g + 2], a.b2[4 * g + 3]};
@@ -295,20 +298,20 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
-    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc2(CodecArgs a) {
-    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc3(CodecArgs a) {
-    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec3(CodecArgs a) {
-    codec_stage<SrcDec<128, 128>, 128, CODEC_TT_DEC3>(
+    codec_stage<SrcDec<128, 128>, 128, CODEC_TT_DEC3, CODEC_RS_DEC3>(
         a, SrcDec<128, 128>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec2(CodecArgs a) {
-    codec_stage<SrcDec<128, 64>, 64, CODEC_TT_DEC2>(
+    codec_stage<SrcDec<128, 64>, 64, CODEC_TT_DEC2, CODEC_RS_DEC2>(
         a, SrcDec<128, 64>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec1_out(CodecArgs a) { codec_dec_out<CODEC_TT_DEC1>(a); }
