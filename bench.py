@@ -156,8 +156,20 @@ def measured_traffic(kernel, grid):
     return None, None
 
 
-def cpu_baseline(cfg, blob, offs, x_bits, budget_s):
-    """The oracle (fp32 C + OpenMP) on the host cores, one frame at a time."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(cfg, blob, offs, x_bits, budget_s, batch):
+    """The oracle (fp32 C + OpenMP) on the host cores: batch-1 frames (median
+    of up to 5 within the budget), then the whole batch once if the batch-1
+    median says it fits the remaining budget."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
@@ -165,19 +177,30 @@ def cpu_baseline(cfg, blob, offs, x_bits, budget_s):
     O.set_threads(threads)
     w = O.f16bits_to_f32(blob)
     n = cfg.H * cfg.W
-    x = O.f16bits_to_f32(x_bits[:n * cfg.dim]).reshape(n, cfg.dim)
-    c = O.cfg(cfg.dim, cfg.n_heads, cfg.head_dim, cfg.n_experts, cfg.H, cfg.W, 1, True)
+    c1 = O.cfg(cfg.dim, cfg.n_heads, cfg.head_dim, cfg.n_experts, cfg.H, cfg.W, 1, True)
+    x1 = O.f16bits_to_f32(x_bits[:n * cfg.dim]).reshape(n, cfg.dim)
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
         t0 = time.perf_counter()
-        O.forward(c, w, list(offs), x)
+        O.forward(c1, w, list(offs), x1)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    return {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} frame(s) of the same workload at batch 1 (8160 tokens x "
-                      f"{cfg.n_blocks} blocks each), median {med * 1e3:.1f} ms/frame; fp32 oracle "
-                      f"(oracle/oracle.c) with OpenMP, host CPU: {platform.processor() or platform.machine()}"}
+    out = {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads, "kind": "port",
+           "cpu": cpu_model(), "omp_threads": O.max_threads()}
+    sample = (f"{len(times)} frame(s) at batch 1 (8160 tokens x {cfg.n_blocks} blocks each), median "
+              f"{med * 1e3:.1f} ms/frame")
+    left = budget_s * 2 - (time.perf_counter() - t_start)
+    if batch > 1 and med * batch < left:
+        cb = O.cfg(cfg.dim, cfg.n_heads, cfg.head_dim, cfg.n_experts, cfg.H, cfg.W, batch, True)
+        xb = O.f16bits_to_f32(x_bits[:batch * n * cfg.dim]).reshape(batch * n, cfg.dim)
+        t0 = time.perf_counter()
+        O.forward(cb, w, list(offs), xb)
+        tb = time.perf_counter() - t0
+        out["batch"] = {"frames": batch, "s": round(tb, 3), "frames_per_s": round(batch / tb, 4)}
+        sample += f"; the batch of {batch} once, {tb:.2f} s"
+    out["sample"] = sample + f"; fp32 oracle (oracle/oracle.c) with OpenMP on {threads} threads, host CPU: {cpu_model()}"
+    return out
 
 
 def main():
@@ -328,7 +351,7 @@ def main():
 
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle)")
-        out["cpu_baseline"] = cpu_baseline(cfg, blob, offs, x.reshape(-1), args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline(cfg, blob, offs, x.reshape(-1), args.cpu_budget, B)
     else:
         out["cpu_baseline"] = None
     hip.free(dx)
