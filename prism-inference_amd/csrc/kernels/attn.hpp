@@ -21,7 +21,8 @@
  *     O^T is normalised, rounded to fp16 and kept in registers until every
  *     wave has finished reading xs; then all heads' O^T go to xs.
  *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x from os (fp16 round),
- *     store; the result also overwrites the lane's residual in os.
+ *     written over the lane's residual in os; the finished tile leaves as
+ *     whole 512-byte rows at the very end (16 bytes per lane).
  *  5. Routed variants (NPT > 0, the block chain's MoE blocks) route that
  *     output tile from os: waves 0-3 each take 16 tokens through
  *     LN2 + router GEMM + argmax (route_token, whose W_r fragments continue
@@ -364,24 +365,19 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int sl = 16 * t + l16;
-        const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
-        const bool vt = gy < a.H && gx < a.W;
-        uint16_t* orow = out + (int64_t)(vt ? gy * a.W + gx : 0) * DIM;
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
             const int ch = (wave * ORT + r) * 16 + 4 * g;
             h4* xr = reinterpret_cast<h4*>(os + sl * LDS + ch); /* this lane's residual, read once */
-            /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding) */
-            const h4 y = add_f16x4(cvt_h4(acc[r][t]), *xr);
-            if (vt) *reinterpret_cast<h4*>(orow + ch) = y;
-            /* the tile stays on chip for routing, over its residual */
-            if constexpr (NPT > 0) *xr = y;
+            /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding), over
+             * the residual: the tile leaves the CU as whole rows (below) */
+            *xr = add_f16x4(cvt_h4(acc[r][t]), *xr);
         }
     }
+    __syncthreads(); /* y tile complete in os */
 
     /* ---- 5. fused routing (moe_router.comp.glsl:24-52 + counting sort) -- */
     if constexpr (NPT > 0) {
-        __syncthreads(); /* y tile complete in os */
         if (routes) {    /* wave w: tokens 16w..16w+15, all experts */
             const int sl = 16 * wave + l16;
             const int sy = wy * 8 + (sl >> 3), sx = wxx * 8 + (sl & 7);
@@ -415,6 +411,23 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                 const int slot = r_base[e] + r_rank[threadIdx.x];
                 if (slot < a.cap) a.perm[(int64_t)e * a.cap + slot] = token;
             }
+        }
+    }
+
+    /* ---- 6. y rows out, 16 bytes per lane (a wave store covers whole rows);
+     * last, so no load above waits behind them (vmcnt counts both) */
+    {
+        constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
+        constexpr int RPS = 64 / CPR; /* rows per wave store    */
+        static_assert(64 % CPR == 0 && SPW % RPS == 0, "row store shape");
+#pragma unroll
+        for (int it = 0; it < SPW / RPS; ++it) {
+            const int sl = wave * SPW + it * RPS + lane / CPR;
+            const int c8 = (lane % CPR) * 8;
+            const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
+            if (gy < a.H && gx < a.W)
+                *reinterpret_cast<h8*>(out + (int64_t)(gy * a.W + gx) * DIM + c8) =
+                    *reinterpret_cast<const h8*>(os + sl * LDS + c8);
         }
     }
 }

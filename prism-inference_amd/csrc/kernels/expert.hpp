@@ -27,12 +27,32 @@
  *
  * GEMMs are C^T = W * A^T (weights as the A operand, tokens as columns), so a
  * lane's accumulator holds 4 consecutive channels of one token: 8-byte LDS
- * writes for the GELU tile and 8-byte global stores for the output rows,
- * scattered straight back to the token's HWC position (fused unpermute). The
- * raw rows stay in LDS for the residual.
+ * writes for the GELU tile and for the output tile, which the epilogue adds
+ * onto the raw rows kept in LDS for the residual and then scatters back to
+ * the tokens' HWC positions as whole 512-byte rows, 16 bytes per lane (fused
+ * unpermute; one store instruction covers two rows instead of 16 tokens x
+ * 32 bytes).
  */
 #pragma once
 #include "common.hpp"
+
+/* Writes the output tile (BM rows in LDS, padded stride DIM + 8) to the
+ * rows of its tokens: each wave stores BM/NW rows, 16 bytes per lane, so one
+ * instruction covers 1 KiB of whole rows instead of 16 tokens x 32 bytes. */
+template <int DIM, int BM, int NW>
+__device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile, const int* tok, int wave, int lane) {
+    constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
+    constexpr int RPS = 64 / CPR; /* rows per wave store    */
+    static_assert(64 % CPR == 0 && (BM / NW) % RPS == 0, "store shape");
+#pragma unroll
+    for (int it = 0; it < BM / NW / RPS; ++it) {
+        const int r = wave * (BM / NW) + it * RPS + lane / CPR;
+        const int c8 = (lane % CPR) * 8;
+        const int tk = tok[r];
+        if (tk >= 0)
+            *reinterpret_cast<h8*>(out + (int64_t)tk * DIM + c8) = *reinterpret_cast<const h8*>(tile + r * (DIM + 8) + c8);
+    }
+}
 
 template <int DIM, int BM, int NW>
 __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
@@ -208,21 +228,17 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             }
             sched_fence();
         }
-        /* epilogue: bias, fp16 round, + h (fp16 round), scatter to token rows */
+        /* epilogue: y = r16(W2 g + b2), out = y + h in fp16 (one rounding),
+         * written over the lane's own residual in hs, then whole rows out */
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            const int tk = tok[16 * t + l16];
-            if (tk >= 0) {
-                const int64_t base = (int64_t)tk * DIM;
+        for (int t = 0; t < TT; ++t)
 #pragma unroll
-                for (int r = 0; r < RT; ++r) {
-                    const int ch = (wave * RT + r) * 16 + 4 * g;
-                    const h4 hin = *reinterpret_cast<const h4*>(hs + (16 * t + l16) * LDS + ch);
-                    /* y = r16(W2 g + b2); out = y + h in fp16 (one rounding) */
-                    *reinterpret_cast<h4*>(a.out + base + ch) = add_f16x4(cvt_h4(acc[r][t]), hin);
-                }
+            for (int r = 0; r < RT; ++r) {
+                h4* hp = reinterpret_cast<h4*>(hs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g);
+                *hp = add_f16x4(cvt_h4(acc[r][t]), *hp);
             }
-        }
+        __syncthreads();
+        expert_store_rows<DIM, BM, NW>(a.out, hs, tok, wave, lane);
     }
 
 }
