@@ -165,9 +165,11 @@ __device__ __forceinline__ h4 cvt_h4(f4 v) {
  * channels per lane, in two steps so a kernel can put every row load in
  * flight before it does any math: ln_load fetches the lane's 16 halfs of a
  * row (zeros for an invalid row), ln_store normalises them into `dst` (and
- * copies the raw values to `raw_dst` if given). Two-pass mean / biased
- * variance in fp32; output rounded to fp16; invalid rows are written as
- * zeros. g and b live in LDS.
+ * copies the raw values to `raw_dst` if given). Lane i of a row holds
+ * channels 8i..8i+7 and DIM/2+8i..+7, so each of the two 16-byte loads of a
+ * wave reads contiguous half rows (whole cache lines, not every other 16
+ * bytes of them). Two-pass mean / biased variance in fp32; output rounded to
+ * fp16; invalid rows are written as zeros. g and b live in LDS.
  */
 /* LayerNorm building blocks (biased variance, eps 1e-5, fp32 statistics):
  * the sum and the sum of squares of fp16 values come straight from the fp16
@@ -201,12 +203,11 @@ struct RowChunk {
 template <int DIM>
 __device__ __forceinline__ RowChunk ln_load(const uint16_t* row, bool valid) {
     constexpr int LPS = DIM / 16;
-    const int c0 = (lane_id() % LPS) * 16;
+    const int ca = (lane_id() % LPS) * 8, cb = ca + DIM / 2;
     RowChunk r{h8{}, h8{}};
     if (valid) {
-        const h8* p = reinterpret_cast<const h8*>(row + c0);
-        r.a0 = p[0];
-        r.a1 = p[1];
+        r.a0 = *reinterpret_cast<const h8*>(row + ca);
+        r.a1 = *reinterpret_cast<const h8*>(row + cb);
     }
     return r;
 }
@@ -215,11 +216,10 @@ template <int DIM>
 __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const float* g, const float* b,
                                          f16* dst, f16* raw_dst) {
     constexpr int LPS = DIM / 16;
-    const int c0 = (lane_id() % LPS) * 16;
+    const int ca = (lane_id() % LPS) * 8, cb = ca + DIM / 2;
     if (raw_dst) {
-        h8* rd = reinterpret_cast<h8*>(raw_dst + c0);
-        rd[0] = rc.a0;
-        rd[1] = rc.a1;
+        *reinterpret_cast<h8*>(raw_dst + ca) = rc.a0;
+        *reinterpret_cast<h8*>(raw_dst + cb) = rc.a1;
     }
     float s = 0.f, q = 0.f;
     moments8(rc.a0, s, q);
@@ -232,14 +232,14 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const f
     h8 o0, o1;
 #pragma unroll
     for (int j = 0; j < 8; j += 4) {
-        const f4 n0 = {ln_apply(rc.a0[j], inv, nmi, g[c0 + j], b[c0 + j]),
-                       ln_apply(rc.a0[j + 1], inv, nmi, g[c0 + j + 1], b[c0 + j + 1]),
-                       ln_apply(rc.a0[j + 2], inv, nmi, g[c0 + j + 2], b[c0 + j + 2]),
-                       ln_apply(rc.a0[j + 3], inv, nmi, g[c0 + j + 3], b[c0 + j + 3])};
-        const f4 n1 = {ln_apply(rc.a1[j], inv, nmi, g[c0 + 8 + j], b[c0 + 8 + j]),
-                       ln_apply(rc.a1[j + 1], inv, nmi, g[c0 + 9 + j], b[c0 + 9 + j]),
-                       ln_apply(rc.a1[j + 2], inv, nmi, g[c0 + 10 + j], b[c0 + 10 + j]),
-                       ln_apply(rc.a1[j + 3], inv, nmi, g[c0 + 11 + j], b[c0 + 11 + j])};
+        const f4 n0 = {ln_apply(rc.a0[j], inv, nmi, g[ca + j], b[ca + j]),
+                       ln_apply(rc.a0[j + 1], inv, nmi, g[ca + j + 1], b[ca + j + 1]),
+                       ln_apply(rc.a0[j + 2], inv, nmi, g[ca + j + 2], b[ca + j + 2]),
+                       ln_apply(rc.a0[j + 3], inv, nmi, g[ca + j + 3], b[ca + j + 3])};
+        const f4 n1 = {ln_apply(rc.a1[j], inv, nmi, g[cb + j], b[cb + j]),
+                       ln_apply(rc.a1[j + 1], inv, nmi, g[cb + j + 1], b[cb + j + 1]),
+                       ln_apply(rc.a1[j + 2], inv, nmi, g[cb + j + 2], b[cb + j + 2]),
+                       ln_apply(rc.a1[j + 3], inv, nmi, g[cb + j + 3], b[cb + j + 3])};
         const h4 p0 = cvt_h4(n0), p1 = cvt_h4(n1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -253,7 +253,6 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const f
     const unsigned int keep = valid ? 0xffffffffu : 0u;
     w0 &= keep;
     w1 &= keep;
-    h8* d = reinterpret_cast<h8*>(dst + c0);
-    d[0] = __builtin_bit_cast(h8, w0);
-    d[1] = __builtin_bit_cast(h8, w1);
+    *reinterpret_cast<h8*>(dst + ca) = __builtin_bit_cast(h8, w0);
+    *reinterpret_cast<h8*>(dst + cb) = __builtin_bit_cast(h8, w1);
 }
