@@ -278,8 +278,9 @@ def main():
     kname = "prism_attn_d256_r4"
     traffic, traffic_src = measured_traffic(kname, attn_grid) if cfg.name == "moe64" else (None, None)
 
-    # ---- projection adapters (next to the chain): per launch at batch B, and the
-    # adapted chain (up -> blocks -> down) as one graph step
+    # ---- projection adapters: the stage launches at batch B, and the adapted
+    # chain (up -> blocks -> down, the projections fused into the first and
+    # last launches) as one graph step
     ablob, aoffs = P.synth_adapters(desc, seed=0)
     eng.load_adapters(ablob, aoffs)
     I = aoffs.in_dim
@@ -298,7 +299,9 @@ def main():
                 "down_hbm_frac": round(proj_bytes / (t_dn * 1e-3) / HBM_PEAK, 4),
                 "bytes_per_launch": proj_bytes,
                 "adapted_chain_ms_per_step": round(ms_ad, 5),
-                "note": "pw_project 128->256 (+ReLU) and 256->128 around the 16 blocks, batch " + str(B)}
+                "note": "up_ms/down_ms: the pw_project 128->256 (+ReLU) and 256->128 stage launches at batch "
+                        + str(B) + "; the adapted chain runs them fused into the first attention and the last "
+                        "expert launch"}
     for ptr in (proj, ax, ay):
         hip.free(ptr)
     log("[bench] end-to-end frame and codec stages")

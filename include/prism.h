@@ -256,7 +256,10 @@ int prism_project_down(prism_ctx* ctx, const prism_project_push* p, void* featur
 
 /* The transformer section of the reference's end-to-end frame
  * (prism_moe_bench.cpp:408-444): up-projection, every block, down-projection.
- * in and out: device fp16 [batch][H*W][in_dim] (in is not modified).
+ * in and out: device fp16 [batch][H*W][in_dim] (in is not modified). The
+ * up-projection runs inside the first block's attention launch and the
+ * down-projection inside the last block's expert launch; the result is
+ * bit-identical to prism_project_up, prism_forward, prism_project_down.
  * _graph replays a captured hipGraph like prism_forward_graph. */
 int prism_forward_adapted(prism_ctx* ctx, const void* in, void* out, int32_t batch,
                           void* stream);

@@ -76,7 +76,7 @@ struct prism_ctx {
     int ws_batch = 0;
     uint16_t* ws_attn = nullptr;
     uint16_t* ws_scratch = nullptr;
-    uint16_t* ws_io[2] = {};      /* adapted chain: projected input / chain output */
+    uint16_t* ws_io = nullptr;    /* adapted chain: 256-channel rows between blocks */
     int32_t* ws_assign = nullptr; /* [n_blocks][n] */
     int32_t* ws_counts = nullptr; /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
     int32_t* ws_perm = nullptr;   /* per half-chain j: [N][its tokens], back to back */

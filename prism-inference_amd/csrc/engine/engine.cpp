@@ -166,7 +166,7 @@ static void drop_adapters(prism_ctx* c) {
 static void drop_workspace(prism_ctx* c) {
     if (c->ws) (void)hipFree(c->ws);
     c->ws = nullptr;
-    c->ws_io[0] = c->ws_io[1] = nullptr;
+    c->ws_io = nullptr;
     c->ws_batch = 0;
     c->ws_tokens = 0;
 }
@@ -447,9 +447,13 @@ struct RouteOut {
 };
 
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
-                 hipStream_t s, const RouteOut* route = nullptr) {
+                 hipStream_t s, const RouteOut* route = nullptr, bool up = false) {
     const int D = c->desc.dim;
     AttnArgs a{};
+    if (up) { /* the adapted chain's first block: 128-channel input rows */
+        a.up_w = c->up_w;
+        a.up_b = c->up_b;
+    }
     a.in = in;
     a.out = out;
     a.wqkv = k.wqkv;
@@ -459,6 +463,7 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     a.ln_g = k.ln1_g;
     a.ln_b = k.ln1_b;
     a.frame_elems = (int64_t)H * W * D;
+    a.in_frame_elems = (int64_t)H * W * (up ? c->aoffs.in_dim : D);
     a.H = H;
     a.W = W;
     a.wx = (W + 7) / 8;
@@ -518,9 +523,13 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
 }
 
 int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, const int32_t* counts,
-                    const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1) {
+                    const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1, bool dn = false) {
     const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
     ExpertArgs a{};
+    if (dn) { /* the adapted chain's last block: 128-channel output rows */
+        a.dn_w = c->down_w;
+        a.dn_b = c->down_b;
+    }
     a.in = in;
     a.out = out;
     a.ln_g = k.ln2_g;
@@ -741,8 +750,8 @@ extern "C" int prism_project_down(prism_ctx* c, const prism_project_push* p, voi
 
 /* io: also the two chain-input/output buffers of the adapted chain */
 static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
-    if (c->ws && c->ws_batch >= batch && (!io || c->ws_io[0])) return PRISM_OK;
-    io = io || (c->ws && c->ws_io[0]); /* keep them once allocated */
+    if (c->ws && c->ws_batch >= batch && (!io || c->ws_io)) return PRISM_OK;
+    io = io || (c->ws && c->ws_io); /* keep them once allocated */
     drop_graph(c);
     drop_workspace(c);
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
@@ -755,7 +764,6 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
     const size_t o_cnt = ar.take((size_t)CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE * 4);
     const size_t o_perm = ar.take((size_t)N * n * 4);
     const size_t o_io0 = ar.take(io ? (size_t)n * D * 2 : 0);
-    const size_t o_io1 = ar.take(io ? (size_t)n * D * 2 : 0);
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, ar.off);
     if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for the workspace: %s", ar.off, hipGetErrorString(e));
@@ -773,8 +781,7 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
     c->ws_assign = reinterpret_cast<int32_t*>(b + o_asg);
     c->ws_counts = reinterpret_cast<int32_t*>(b + o_cnt);
     c->ws_perm = reinterpret_cast<int32_t*>(b + o_perm);
-    c->ws_io[0] = io ? reinterpret_cast<uint16_t*>(b + o_io0) : nullptr;
-    c->ws_io[1] = io ? reinterpret_cast<uint16_t*>(b + o_io1) : nullptr;
+    c->ws_io = io ? reinterpret_cast<uint16_t*>(b + o_io0) : nullptr;
     c->counts_dirty = false; /* zero-filled above */
     return PRISM_OK;
 }
@@ -790,8 +797,13 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
  * next prism_forward / prism_forward_graph call clears the counters first.
  * With 2 * CHAIN_SPLIT_FRAMES frames or more the batch runs as sub-chains
  * (own counter rows, own bucket region, disjoint frames of every buffer). */
+/* Sub-chain j: frames [f0, f0 + nf) through every block, in -> out (this
+ * sub-chain's frames). adapted: in and out hold 128-channel rows; block 0's
+ * attention runs the up-projection in its prologue and the last block's
+ * expert stage the down-projection in its epilogue, the blocks in between
+ * ping-pong through the 256-channel workspace (ws_io, ws_scratch). */
 static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t* in, uint16_t* out,
-                            hipStream_t s) {
+                            hipStream_t s, bool adapted = false) {
     const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w, D = c->desc.dim;
     const int N = c->desc.n_experts;
     const bool moe = N > 1;
@@ -801,6 +813,7 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
     int32_t* perm = c->ws_perm + (size_t)N * t0; /* this half's buckets: [N][n] */
     uint16_t* attn = c->ws_attn + t0 * D;
     uint16_t* scratch = c->ws_scratch + t0 * D;
+    uint16_t* mid = adapted ? c->ws_io + t0 * D : out; /* 256-channel stand-in for `out` */
     if (moe && NB == 1) {
         const int rc = enqueue_zero(c, counts0, (int32_t)row, s);
         if (rc) return rc;
@@ -808,19 +821,20 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
     const uint16_t* src = in;
     for (int b = 0; b < NB; ++b) {
         const DevBlock& k = c->blocks[b];
-        uint16_t* dst = ((NB - 1 - b) % 2 == 0) ? out : scratch;
+        const bool first = adapted && b == 0, last = adapted && b == NB - 1;
+        uint16_t* dst = last ? out : ((NB - 1 - b) % 2 == 0) ? mid : scratch;
         if (moe) {
             int32_t* counts = counts0 + (size_t)b * row;
             const RouteOut ro{c->ws_assign + (size_t)b * n_all + t0, counts, perm, CHAIN_COUNT_STRIDE,
                               NB > 1 ? counts0 + (size_t)((b + 1) % NB) * row : nullptr};
-            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro);
+            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro, first);
             if (rc) return rc;
-            rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE);
+            rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last);
             if (rc) return rc;
         } else {
-            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s);
+            int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, nullptr, first);
             if (rc) return rc;
-            rc = enqueue_experts(c, k, attn, dst, nullptr, nullptr, n, s);
+            rc = enqueue_experts(c, k, attn, dst, nullptr, nullptr, n, s, 1, last);
             if (rc) return rc;
         }
         src = dst;
@@ -828,11 +842,13 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
     return PRISM_OK;
 }
 
-static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s) {
-    const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w, D = c->desc.dim;
+static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s,
+                                bool adapted = false) {
+    const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w;
+    const int64_t D = adapted ? c->aoffs.in_dim : c->desc.dim; /* channels of in and out */
     c->fwd_tokens = (int64_t)batch * T;
     const int S = std::max(1, std::min(CHAIN_SPLIT, batch / CHAIN_SPLIT_FRAMES));
-    if (S == 1) return enqueue_subchain(c, 0, 0, batch, in, out, s);
+    if (S == 1) return enqueue_subchain(c, 0, 0, batch, in, out, s, adapted);
     /* fork: sub-chain j > 0 on sub_stream[j-1], sub-chain 0 on s, then join */
     HIP_TRY(c, hipEventRecord(c->ev_fork, s));
     int rc = PRISM_OK;
@@ -840,7 +856,7 @@ static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out,
         const int f0 = (int)((int64_t)batch * j / S), f1 = (int)((int64_t)batch * (j + 1) / S);
         hipStream_t sj = j ? c->sub_stream[j - 1] : s;
         if (j) HIP_TRY(c, hipStreamWaitEvent(sj, c->ev_fork, 0));
-        const int r = enqueue_subchain(c, j, f0, f1 - f0, in + f0 * T * D, out + f0 * T * D, sj);
+        const int r = enqueue_subchain(c, j, f0, f1 - f0, in + f0 * T * D, out + f0 * T * D, sj, adapted);
         if (!rc) rc = r;
         if (j) HIP_TRY(c, hipEventRecord(c->ev_join[j - 1], sj));
     }
@@ -866,9 +882,10 @@ static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
     return PRISM_OK;
 }
 
-/* The chain (CHAIN_BLOCKS); wrapped in the projection adapters (CHAIN_ADAPTED):
- * up(in -> ws_io[0]), blocks(ws_io[0] -> ws_io[1]), down(ws_io[1] -> out);
- * and that inside the encoder and decoder (CHAIN_E2E): encode(frame ->
+/* The chain (CHAIN_BLOCKS); wrapped in the projection adapters (CHAIN_ADAPTED:
+ * the up-projection fused into the first block's attention, the
+ * down-projection into the last block's expert stage, 128-channel in and
+ * out); and that inside the encoder and decoder (CHAIN_E2E): encode(frame ->
  * cbott), adapted chain(cbott -> cchain), decode(cchain -> display). */
 static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, int mode, hipStream_t s) {
     if (mode == CHAIN_BLOCKS) return enqueue_forward_impl(c, in, out, batch, s);
@@ -878,12 +895,7 @@ static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int ba
         if (!rc) rc = codec_enqueue_decode(c, c->cchain, out, batch, s);
         return rc;
     }
-    const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
-    int rc = enqueue_project(c, true, in, c->ws_io[0], n, s);
-    if (rc) return rc;
-    rc = enqueue_forward_impl(c, c->ws_io[0], c->ws_io[1], batch, s);
-    if (rc) return rc;
-    return enqueue_project(c, false, c->ws_io[1], out, n, s);
+    return enqueue_forward_impl(c, in, out, batch, s, true);
 }
 
 static int mode_ready(prism_ctx* c, int mode, int batch) {

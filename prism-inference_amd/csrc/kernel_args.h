@@ -43,6 +43,12 @@ typedef struct AttnArgs {
     int32_t cap;          /* tokens in the launch = batch * H * W         */
     int32_t count_stride; /* ints between counters (a cache line apart in the chain) */
     int32_t pad_;
+    /* fused up-projection (first block of the adapted chain): if set, `in`
+     * holds 128-channel rows (in_frame_elems per frame) and the block's input
+     * is x = r16(ReLU(W_up e + b_up)), computed in the prologue */
+    const uint16_t* up_w; /* packed [dim/16][128/32]                    */
+    const float* up_b;    /* [dim]                                       */
+    int64_t in_frame_elems; /* H*W*dim, or H*W*128 with up_w               */
 } AttnArgs;
 
 typedef struct RouterArgs {
@@ -77,6 +83,11 @@ typedef struct ExpertArgs {
     int32_t n_experts;
     int32_t cap;
     int32_t count_stride;
+    /* fused down-projection (last block of the adapted chain): if set, the
+     * block output y goes through r16(W_dn y + b_dn) and `out` holds
+     * 128-channel rows */
+    const uint16_t* dn_w; /* packed [128/16][dim/32]                    */
+    const float* dn_b;    /* [128]                                       */
 } ExpertArgs;
 
 typedef struct ProjArgs {

@@ -7,7 +7,10 @@
  *
  *  1. LN1 of the window's 64 slots -> xs (LDS, fp16), the raw rows -> os
  *     (they are the residual; the out-proj's epilogue reads them from there,
- *     so x is fetched from HBM once). Padded slots are zero.
+ *     so x is fetched from HBM once). Padded slots are zero. With a fused
+ *     up-projection (the adapted chain's first block) the input rows have 128
+ *     channels and x = r16(ReLU(W_up e + b_up)) is computed into os first
+ *     (shaders/pw_project_128to256.comp.glsl:25-37, as project.hpp).
  *  2. Wave w owns heads w and w+4 (8-wave variant: head w). Per head, one
  *     MFMA GEMM pass over the model dim produces Q^T and K^T (rows = channel,
  *     cols = token) and V
@@ -121,7 +124,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     const int wi = wg - frame * a.windows_per_frame;
     const int wy = wi / a.wx;
     const int wxx = wi - wy * a.wx;
-    const uint16_t* in = a.in + (int64_t)frame * a.frame_elems;
+    const uint16_t* in = a.in + (int64_t)frame * a.in_frame_elems;
     uint16_t* out = a.out + (int64_t)frame * a.frame_elems;
 
     const FragSrc src_qkv(a.wqkv, 3u * DIM * DIM * 2u);
@@ -141,14 +144,41 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     constexpr int SPI = 64 / LPS;       /* slots per wave iteration */
     constexpr int SPW = 64 / NW;        /* slots per wave           */
     constexpr int IT = SPW / SPI;
+    /* fused up-projection: the window's 128-channel input rows (16 chunks
+     * of 16 bytes each, EPT per thread) and this wave's W_up fragments */
+    constexpr int UIN = 128, UKS = UIN / 32, UPR = DIM / 16 / NW, EPT = 64 * (UIN / 8) / NT;
+    static_assert(UPR >= 1 && EPT >= 1, "up-projection shape");
+    const bool up = a.up_w != nullptr; /* uniform over the launch */
     RowChunk rc[IT];
     bool valid[IT];
+    h8 erow[EPT];
+    h8 wup[UPR][UKS];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int s = wave * SPW + it * SPI + lane / LPS;
         const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
         valid[it] = gy < a.H && gx < a.W;
-        rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
+    }
+    if (!up) {
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int s = wave * SPW + it * SPI + lane / LPS;
+            const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
+            rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const int q = threadIdx.x + k * NT, sl = q / (UIN / 8), c8 = (q % (UIN / 8)) * 8;
+            const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
+            const bool ok = gy < a.H && gx < a.W;
+            erow[k] = ok ? *reinterpret_cast<const h8*>(in + (int64_t)(gy * a.W + gx) * UIN + c8) : h8{};
+        }
+        const FragSrc src_up(a.up_w, (unsigned)(DIM * UIN * 2));
+#pragma unroll
+        for (int ks = 0; ks < UKS; ++ks)
+#pragma unroll
+            for (int r = 0; r < UPR; ++r) wup[r][ks] = src_up.load((wave * UPR + r) * UKS + ks, lane * 16);
     }
     sched_fence();
 
@@ -177,10 +207,62 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     if constexpr (NPT > 0)
         for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
     __syncthreads(); /* parameters staged */
+    if (!up) {
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
-        ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + row, os + row); /* os: the raw rows (residual) */
+        for (int it = 0; it < IT; ++it) {
+            const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + row, os + row); /* os: the raw rows (residual) */
+        }
+    } else {
+        /* x = r16(ReLU(W_up e + b_up)) for the window's slots, the same
+         * arithmetic as prism_project_up_d* (bias in the accumulator, k-steps
+         * in order), into os as the raw rows; padded slots are zero. The 128-
+         * channel rows are staged in xs first (B operands). */
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const int q = threadIdx.x + k * NT, sl = q / (UIN / 8), c8 = (q % (UIN / 8)) * 8;
+            *reinterpret_cast<h8*>(xs + sl * LDS + c8) = erow[k];
+        }
+        __syncthreads();
+        f4 uacc[UPR][4];
+#pragma unroll
+        for (int r = 0; r < UPR; ++r) {
+            const int ch = (wave * UPR + r) * 16 + 4 * g;
+            const f4 bb = {a.up_b[ch], a.up_b[ch + 1], a.up_b[ch + 2], a.up_b[ch + 3]};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) uacc[r][t] = bb;
+        }
+#pragma unroll
+        for (int ks = 0; ks < UKS; ++ks)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const h8 xf = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+#pragma unroll
+                for (int r = 0; r < UPR; ++r) uacc[r][t] = mfma_16x16x32(wup[r][ks], xf, uacc[r][t]);
+            }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int sl = 16 * t + l16;
+            const bool ok = wy * 8 + (sl >> 3) < a.H && wxx * 8 + (sl & 7) < a.W;
+#pragma unroll
+            for (int r = 0; r < UPR; ++r) {
+                f4 v = uacc[r][t];
+                /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+                const h4 x4 = cvt_h4(v);
+                *reinterpret_cast<h4*>(os + sl * LDS + (wave * UPR + r) * 16 + 4 * g) = ok ? x4 : h4{};
+            }
+        }
+        __syncthreads(); /* x complete in os; the staging in xs is dead */
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+            const int ca = (lane % LPS) * 8;
+            const RowChunk xr{*reinterpret_cast<const h8*>(os + row + ca),
+                              *reinterpret_cast<const h8*>(os + row + ca + DIM / 2)};
+            ln_store<DIM>(xr, valid[it], s_g, s_b, xs + row, nullptr);
+        }
     }
     __syncthreads();
 

@@ -36,12 +36,13 @@
 #pragma once
 #include "common.hpp"
 
-/* Writes the output tile (BM rows in LDS, padded stride DIM + 8) to the
- * rows of its tokens: each wave stores BM/NW rows, 16 bytes per lane, so one
- * instruction covers 1 KiB of whole rows instead of 16 tokens x 32 bytes. */
-template <int DIM, int BM, int NW>
+/* Writes the output tile (BM rows of C channels in LDS, row stride STRIDE
+ * halfs) to the rows of its tokens: each wave stores BM/NW rows, 16 bytes
+ * per lane, so one instruction covers 1 KiB of whole rows instead of 16
+ * tokens x 32 bytes. */
+template <int C, int STRIDE, int BM, int NW>
 __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile, const int* tok, int wave, int lane) {
-    constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
+    constexpr int CPR = C / 8;    /* 16-byte chunks per row */
     constexpr int RPS = 64 / CPR; /* rows per wave store    */
     static_assert(64 % CPR == 0 && (BM / NW) % RPS == 0, "store shape");
 #pragma unroll
@@ -50,7 +51,7 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
         const int c8 = (lane % CPR) * 8;
         const int tk = tok[r];
         if (tk >= 0)
-            *reinterpret_cast<h8*>(out + (int64_t)tk * DIM + c8) = *reinterpret_cast<const h8*>(tile + r * (DIM + 8) + c8);
+            *reinterpret_cast<h8*>(out + (int64_t)tk * C + c8) = *reinterpret_cast<const h8*>(tile + r * STRIDE + c8);
     }
 }
 
@@ -228,6 +229,19 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             }
             sched_fence();
         }
+        /* fused down-projection (last block of the adapted chain): W_dn
+         * fragments go out now, while the epilogue below runs */
+        constexpr int DO = 128, DRT = DO / 16 / NW;
+        static_assert(DRT >= 1, "down-projection shape");
+        const bool dn = a.dn_w != nullptr; /* uniform over the launch */
+        h8 wd[DRT][KS];
+        if (dn) {
+            const FragSrc src_dn(a.dn_w, (unsigned)(DO * DIM * 2));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int r = 0; r < DRT; ++r) wd[r][ks] = src_dn.load((wave * DRT + r) * KS + ks, loff);
+        }
         /* epilogue: y = r16(W2 g + b2), out = y + h in fp16 (one rounding),
          * written over the lane's own residual in hs, then whole rows out */
 #pragma unroll
@@ -238,7 +252,37 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
                 *hp = add_f16x4(cvt_h4(acc[r][t]), *hp);
             }
         __syncthreads();
-        expert_store_rows<DIM, BM, NW>(a.out, hs, tok, wave, lane);
+        if (!dn) {
+            expert_store_rows<DIM, LDS, BM, NW>(a.out, hs, tok, wave, lane);
+        } else {
+            /* r16(W_dn y + b_dn) (shaders/pw_project_256to128.comp.glsl:25-32,
+             * the same arithmetic as prism_project_down_d*) from the output
+             * tile in hs into xs (free since GEMM2), then 128-channel rows out */
+            f4 dacc[DRT][TT];
+#pragma unroll
+            for (int r = 0; r < DRT; ++r) {
+                const int ch = (wave * DRT + r) * 16 + 4 * g;
+                const f4 bb = {a.dn_b[ch], a.dn_b[ch + 1], a.dn_b[ch + 2], a.dn_b[ch + 3]};
+#pragma unroll
+                for (int t = 0; t < TT; ++t) dacc[r][t] = bb;
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const h8 yf = *reinterpret_cast<const h8*>(hs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
+#pragma unroll
+                    for (int r = 0; r < DRT; ++r) dacc[r][t] = mfma_16x16x32(wd[r][ks], yf, dacc[r][t]);
+                }
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int r = 0; r < DRT; ++r)
+                    *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + (wave * DRT + r) * 16 + 4 * g) =
+                        cvt_h4(dacc[r][t]);
+            __syncthreads();
+            expert_store_rows<DO, LDS, BM, NW>(a.out, xs, tok, wave, lane);
+        }
     }
 
 }

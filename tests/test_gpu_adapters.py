@@ -135,3 +135,38 @@ def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch):
     moved = float((err.max(axis=1) > MAX_ABS).mean())
     print(f"[adapted] {name}: max {err.max():.3g} mean {err.mean():.3g}, tokens moved > {MAX_ABS}: {moved:.4f}")
     assert err.mean() <= MEAN_ABS and moved <= 0.02
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,nb,H,W,batch", [
+    ("moe16", 2, 20, 28, 4),    # two sub-chains; ragged windows
+    ("moe64", 1, 68, 120, 1),   # one block: up- and down-projection in the same block
+    ("moe64", 3, 68, 120, 1),   # 8-wave kernels
+    ("dense128", 3, 68, 120, 2),
+    ("std256", 2, 16, 16, 5),   # dense d256, sub-chains of 2 and 3 frames
+])
+def test_fused_adapters_equal_the_separate_calls(hip, engine, device_arena, name, nb, H, W, batch):
+    """The adapted chain fuses the up-projection into the first block's
+    attention prologue and the down-projection into the last block's expert
+    epilogue, with the projection kernels' arithmetic: its output is
+    bit-identical to prism_project_up -> the plain chain -> prism_project_down."""
+    cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W)
+    n, D, I = batch * H * W, cfg.dim, a.in_dim
+    x = P.synth_normal(n * I, seed=13).reshape(n, I)
+    feats = device_arena((n * I + 2 * n * D + n * I) * 2 + 64)
+    o_x, o_h, o_g, o_y = 0, n * I, n * I + n * D, n * I + 2 * n * D
+    hip.upload(feats.ptr, x)
+    print(f"[fused] {name} {nb} blocks {H}x{W} batch {batch}", flush=True)
+    assert engine.project(True, engine.project_push(True, H * W, o_x, o_h), feats.ptr, batch) == 0, engine.error()
+    engine.forward(feats.ptr + o_h * 2, feats.ptr + o_g * 2, batch)
+    assert engine.project(False, engine.project_push(False, H * W, o_g, o_y), feats.ptr, batch) == 0, engine.error()
+    hip.sync()
+    ref = hip.download(np.empty(n * I, np.uint16), feats.ptr + o_y * 2)
+    dy = device_arena(n * I * 2)
+    for graph in (False, True, True):
+        hip.memset(dy.ptr, 0xFF, n * I * 2)  # NaN fill: every output row must be written
+        engine.forward(feats.ptr, dy.ptr, batch, graph=graph, adapted=True)
+        hip.sync()
+        got = hip.download(np.empty(n * I, np.uint16), dy.ptr)
+        assert (got == ref).all(), f"graph={graph}: {int((got != ref).sum())} values differ"
+    assert np.isfinite(f16(ref)).all()
