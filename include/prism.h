@@ -175,7 +175,12 @@ int prism_load_weights_file(prism_ctx* ctx, const prism_model_desc* desc,
 /* ---- per-stage launches (one dispatch each) --------------------------- */
 
 /* features: device fp16 arena; aux: device int32 arena. The weight offsets
- * in the push structs must name tensors of a loaded block. */
+ * in the push structs must name tensors of a loaded block. prism_router
+ * writes the assignment, the counts (from zero) and the buckets; it counts
+ * into a row of the context's own, counters 256 bytes apart, and a
+ * one-workgroup launch copies the totals to `counts`, so router and
+ * attention-route calls on one context must not overlap on different
+ * streams. */
 int prism_attn(prism_ctx* ctx, const prism_attn_push* p, void* features, int32_t batch,
                void* stream);
 int prism_router(prism_ctx* ctx, const prism_router_push* p, const void* features,

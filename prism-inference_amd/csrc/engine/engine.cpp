@@ -501,7 +501,7 @@ int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {
 }
 
 int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t* assign, int32_t* counts,
-                   int32_t* perm, int64_t n, hipStream_t s) {
+                   int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride) {
     const int N = c->desc.n_experts;
     RouterArgs a{};
     a.in = in;
@@ -516,8 +516,11 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
     a.n_experts = N;
     a.np = round16(N);
     a.cap = (int32_t)n;
-    /* 2 tiles per wave at frame scale, up to 8 at large batch (fewer global atomics) */
-    a.tiles_per_wave = (int32_t)std::min<int64_t>(8, std::max<int64_t>(2, (n + 16383) / 16384));
+    a.count_stride = count_stride;
+    /* tiles per wave for about 512 workgroups (two per CU): one tile per wave
+     * at frame scale, 4 at batch 16 (measured 8.9 / 22.2 us; more, smaller
+     * workgroups each copy W_r into LDS, fewer leave CUs idle) */
+    a.tiles_per_wave = (int32_t)std::min<int64_t>(ROUTER_MAX_TILES_PER_WAVE, std::max<int64_t>(1, (n + 32767) / 32768));
     const int64_t grid = (n + 64 * a.tiles_per_wave - 1) / (64 * a.tiles_per_wave);
     return launch(c, c->f_router[dim_index(c->desc.dim)][a.np / 16 - 1], (unsigned)grid, a, s);
 }
@@ -635,17 +638,49 @@ extern "C" int prism_attn(prism_ctx* c, const prism_attn_push* p, void* features
                         (hipStream_t)stream);
 }
 
+/* The routing stage calls count into a private row, counters 256 B apart as
+ * in the chain (every workgroup adds to them; adjacent counters would
+ * serialise those atomics), and prism_take_counts then moves the totals to
+ * the caller's contiguous counts, clearing the row for the next call. */
+static int stage_counts_begin(prism_ctx* c, hipStream_t s) {
+    if (!c->stage_counts) {
+        const size_t bytes = sizeof(int32_t) * 64 * CHAIN_COUNT_STRIDE;
+        HIP_TRY(c, hipMalloc((void**)&c->stage_counts, bytes));
+        HIP_TRY(c, hipMemset(c->stage_counts, 0, bytes));
+    }
+    if (c->stage_dirty) {
+        const int rc = enqueue_zero(c, c->stage_counts, 64 * CHAIN_COUNT_STRIDE, s);
+        if (rc) return rc;
+        c->stage_dirty = false;
+    }
+    c->stage_dirty = true; /* until stage_counts_take has been enqueued */
+    return PRISM_OK;
+}
+
+static int stage_counts_take(prism_ctx* c, int32_t* dst, int32_t n, hipStream_t s) {
+    int32_t* src = c->stage_counts;
+    int32_t stride = CHAIN_COUNT_STRIDE;
+    void* params[] = {&src, &stride, &dst, &n};
+    const hipError_t e = hipModuleLaunchKernel(c->f_take, 1, 1, 1, 64, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(take counts): %s", hipGetErrorString(e));
+    c->stage_dirty = false;
+    return PRISM_OK;
+}
+
 extern "C" int prism_router(prism_ctx* c, const prism_router_push* p, const void* features, int32_t* aux,
                             int32_t batch, void* stream) {
     const DevBlock* k = nullptr;
     int rc = check_router(c, p, features, aux, batch, &k);
     if (rc) return rc;
     HIP_TRY(c, hipSetDevice(c->device));
-    rc = enqueue_zero(c, aux + p->count_offset, p->n_experts, (hipStream_t)stream);
+    const hipStream_t s = (hipStream_t)stream;
+    rc = stage_counts_begin(c, s);
     if (rc) return rc;
     const uint16_t* f = static_cast<const uint16_t*>(features);
-    return enqueue_router(c, *k, f + p->input_offset, aux + p->assignment_offset, aux + p->count_offset,
-                          aux + p->perm_offset, (int64_t)batch * p->n_tokens, (hipStream_t)stream);
+    rc = enqueue_router(c, *k, f + p->input_offset, aux + p->assignment_offset, c->stage_counts,
+                        aux + p->perm_offset, (int64_t)batch * p->n_tokens, s, CHAIN_COUNT_STRIDE);
+    if (rc) return rc;
+    return stage_counts_take(c, aux + p->count_offset, p->n_experts, s);
 }
 
 extern "C" int prism_attn_route(prism_ctx* c, const prism_attn_push* pa, const prism_router_push* pr, void* features,
@@ -660,34 +695,14 @@ extern "C" int prism_attn_route(prism_ctx* c, const prism_attn_push* pa, const p
         return fail(c, PRISM_ERR_INVALID, "the router must read the attention output (input_offset %lld != %lld)",
                     (long long)pr->input_offset, (long long)pa->output_offset);
     HIP_TRY(c, hipSetDevice(c->device));
-    /* The kernel counts into a private row, counters 256 B apart as in the
-     * chain (every workgroup adds to them; adjacent counters would serialise
-     * those atomics), and prism_take_counts moves the totals to the caller's
-     * contiguous counts, clearing the row for the next call. */
     const hipStream_t s = (hipStream_t)stream;
-    if (!c->stage_counts) {
-        const size_t bytes = sizeof(int32_t) * 64 * CHAIN_COUNT_STRIDE;
-        HIP_TRY(c, hipMalloc((void**)&c->stage_counts, bytes));
-        HIP_TRY(c, hipMemset(c->stage_counts, 0, bytes));
-    }
-    if (c->stage_dirty) {
-        rc = enqueue_zero(c, c->stage_counts, 64 * CHAIN_COUNT_STRIDE, s);
-        if (rc) return rc;
-        c->stage_dirty = false;
-    }
+    rc = stage_counts_begin(c, s);
+    if (rc) return rc;
     uint16_t* f = static_cast<uint16_t*>(features);
     const RouteOut ro{aux + pr->assignment_offset, c->stage_counts, aux + pr->perm_offset, CHAIN_COUNT_STRIDE, nullptr};
-    c->stage_dirty = true;
     rc = enqueue_attn(c, *ka, f + pa->input_offset, f + pa->output_offset, pa->spatial_h, pa->spatial_w, batch, s, &ro);
     if (rc) return rc;
-    int32_t* src = c->stage_counts;
-    int32_t stride = CHAIN_COUNT_STRIDE, n = pr->n_experts;
-    int32_t* dst = aux + pr->count_offset;
-    void* params[] = {&src, &stride, &dst, &n};
-    const hipError_t e = hipModuleLaunchKernel(c->f_take, 1, 1, 1, 64, 1, 1, 0, s, params, nullptr);
-    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(take counts): %s", hipGetErrorString(e));
-    c->stage_dirty = false;
-    return PRISM_OK;
+    return stage_counts_take(c, aux + pr->count_offset, pr->n_experts, s);
 }
 
 extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* features, int32_t* aux, int32_t batch,

@@ -51,6 +51,10 @@ typedef struct AttnArgs {
     int64_t in_frame_elems; /* H*W*dim, or H*W*128 with up_w               */
 } AttnArgs;
 
+/* Router stage: at most this many 16-token tiles per wave (the LDS tables
+ * are sized for it). */
+#define ROUTER_MAX_TILES_PER_WAVE 8
+
 typedef struct RouterArgs {
     const uint16_t* in;   /* features + input_offset                     */
     const float* ln_g;
@@ -58,14 +62,14 @@ typedef struct RouterArgs {
     const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts are 0 */
     const float* br;      /* [np]; entries >= n_experts are -inf          */
     int32_t* assign;      /* [n_tokens] expert id                         */
-    int32_t* counts;      /* [n_experts] per-expert totals (zero on entry) */
+    int32_t* counts;      /* expert e's total at counts[e * count_stride] (zero on entry) */
     int32_t* perm;        /* [n_experts][cap] token ids bucketed by expert */
     int32_t n_tokens;     /* tokens in this launch (batch * per-frame)     */
     int32_t n_experts;
     int32_t np;           /* n_experts rounded up to 16                    */
     int32_t cap;          /* bucket capacity = n_tokens                    */
     int32_t tiles_per_wave; /* 16-token tiles per wave: WG = 64*tiles tokens */
-    int32_t pad_;
+    int32_t count_stride; /* ints between counters                         */
 } RouterArgs;
 
 typedef struct ExpertArgs {

@@ -6,7 +6,9 @@
  * the per-token math (route_token, route.hpp) gives the expert, the expert id
  * is written per token (:48) and the per-expert count is incremented (:51).
  * The count atomics become a workgroup-local LDS histogram plus one global
- * atomic per (workgroup, expert); each token's LDS
+ * atomic per (workgroup, expert), on counters count_stride ints apart (the
+ * stage call uses a private row with counters 256 B apart, so the atomics of
+ * different experts do not serialise on one cache line); each token's LDS
  * rank then places it in its expert's bucket of `perm`, which is the
  * expert-contiguous segment the grouped expert GEMM consumes.
  *
@@ -25,8 +27,6 @@
  */
 #pragma once
 #include "route.hpp"
-
-#define ROUTER_MAX_TILES_PER_WAVE 8
 
 template <int DIM, int KS>
 __device__ __forceinline__ void router_load_tile(const RouterArgs& a, int token, int g, h8 (&xr)[KS]) {
@@ -89,7 +89,7 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
     __syncthreads();
     if (threadIdx.x < a.n_experts) {
         const int c = hist[threadIdx.x];
-        base[threadIdx.x] = c ? atomicAdd(&a.counts[threadIdx.x], c) : 0;
+        base[threadIdx.x] = c ? atomicAdd(&a.counts[threadIdx.x * a.count_stride], c) : 0;
     }
     __syncthreads();
     for (int j = threadIdx.x; j < wg_tokens; j += 256) {
