@@ -4,12 +4,13 @@
  * Restates shaders/pw_project_128to256.comp.glsl:25-37 (y = r16(W x + b), then
  * ReLU) and shaders/pw_project_256to128.comp.glsl:25-32 (y = r16(W x + b)),
  * which the reference runs one thread per token, as a GEMM over 64-token
- * tiles: C^T = W * X^T with the packed weights as the A operand. A token's
- * row is contiguous (HWC), so a lane's B fragment (token 16t + l16, channels
- * 32ks + 8g .. +7) is one 16-byte global load and the tile needs no LDS.
- * Workgroup = 4 waves; wave w computes output rows [w*OUT/4, +OUT/4) of the
- * tile's 64 tokens, accumulators starting at the bias. The tile's row loads
- * and the wave's weight fragments all go out before the first MFMA.
+ * tiles: C^T = W * X^T with the packed weights as the A operand. A tile's 64
+ * token rows are one contiguous block in and one out (HWC): they pass through
+ * an LDS tile as whole rows, 16 bytes per lane, and the B fragments (token
+ * 16t + l16, channels 32ks + 8g .. +7) are read from there. Workgroup = 4
+ * waves; wave w computes output rows [w*OUT/4, +OUT/4) of the tile's 64
+ * tokens, accumulators starting at the bias. The tile's row loads and the
+ * wave's weight fragments all go out before the first MFMA.
  */
 #pragma once
 #include "common.hpp"
@@ -19,23 +20,26 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
     constexpr int KS = IN / 32;  /* k-steps                     */
     constexpr int RT = OUT / 64; /* 16-row output tiles per wave */
     constexpr int TT = 4;        /* 16-token tiles per workgroup */
-    static_assert(IN % 32 == 0 && OUT % 64 == 0, "shape");
+    constexpr int LI = IN + 8, LO = OUT + 8;  /* padded LDS rows (halfs) */
+    constexpr int EI = 64 * IN / 8 / 256;     /* 16-byte input chunks per thread  */
+    constexpr int EO = 64 * OUT / 8 / 256;    /* 16-byte output chunks per thread */
+    static_assert(IN % 32 == 0 && OUT % 64 == 0 && EI >= 1 && EO >= 1, "shape");
+    __shared__ __attribute__((aligned(16))) f16 tile[64 * (LI > LO ? LI : LO)];
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
     const int64_t tok0 = (int64_t)blockIdx.x * 64;
+    const int rows = (int)min<int64_t>(64, a.n_tokens - tok0);
 
-    h8 xf[TT][KS];
-    bool valid[TT];
+    /* the tile's rows are one contiguous block: 16 bytes per lane, whole
+     * cache lines per wave load; then this wave's weight fragments */
+    h8 xin[EI];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        const int64_t tk = tok0 + 16 * t + l16;
-        valid[t] = tk < a.n_tokens;
-        const uint16_t* row = a.in + (valid[t] ? tk : 0) * IN + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) xf[t][ks] = valid[t] ? *reinterpret_cast<const h8*>(row + 32 * ks) : h8{};
+    for (int k = 0; k < EI; ++k) {
+        const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
+        xin[k] = r < rows ? *reinterpret_cast<const h8*>(a.in + (tok0 + r) * IN + c8) : h8{};
     }
     const FragSrc src(a.w, (unsigned)(OUT * IN * 2));
     h8 wf[RT][KS];
@@ -43,9 +47,14 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int r = 0; r < RT; ++r) wf[r][ks] = src.load((wave * RT + r) * KS + ks, lane * 16);
-    sched_fence();
+#pragma unroll
+    for (int k = 0; k < EI; ++k) {
+        const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
+        *reinterpret_cast<h8*>(tile + r * LI + c8) = xin[k];
+    }
+    __syncthreads();
 
-    f4 acc[RT][TT];
+    f4 acc[RT][TT]; /* starts at the bias */
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const int ch = (wave * RT + r) * 16 + 4 * g;
@@ -56,14 +65,14 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
+        for (int t = 0; t < TT; ++t) {
+            const h8 xf = *reinterpret_cast<const h8*>(tile + (16 * t + l16) * LI + 32 * ks + 8 * g);
 #pragma unroll
-            for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t][ks], acc[r][t]);
-
+            for (int r = 0; r < RT; ++r) acc[r][t] = mfma_16x16x32(wf[r][ks], xf, acc[r][t]);
+        }
+    __syncthreads(); /* every wave has read the input tile */
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        if (!valid[t]) continue;
-        uint16_t* orow = a.out + (tok0 + 16 * t + l16) * OUT;
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f4 v = acc[r][t];
@@ -72,8 +81,13 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
             }
-            *reinterpret_cast<h4*>(orow + (wave * RT + r) * 16 + 4 * g) = cvt_h4(v);
+            *reinterpret_cast<h4*>(tile + (16 * t + l16) * LO + (wave * RT + r) * 16 + 4 * g) = cvt_h4(v);
         }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < EO; ++k) {
+        const int q = threadIdx.x + 256 * k, r = q / (OUT / 8), c8 = (q % (OUT / 8)) * 8;
+        if (r < rows) *reinterpret_cast<h8*>(a.out + (tok0 + r) * OUT + c8) = *reinterpret_cast<const h8*>(tile + r * LO + c8);
     }
 }
 
