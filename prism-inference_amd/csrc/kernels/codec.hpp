@@ -144,11 +144,16 @@ __device__ __forceinline__ void codec_pixels(const CodecArgs& a, int wave, int l
     }
 }
 
-/* One stage: GEMM, ReLU, fp16, NHWC store. */
+/* One stage: GEMM, ReLU, fp16, NHWC store. The workgroup's pixels are
+ * consecutive, so its output is one contiguous block: the tile is assembled
+ * in LDS and leaves as whole pixel rows, 16 bytes per lane (a store straight
+ * from the accumulators writes 16 pixels x 32 bytes per instruction). */
 template <class Src, int COUT, int TT, int RS>
 __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) {
     constexpr int RTALL = COUT / 16, RT = RTALL / RS;
     static_assert(COUT % 16 == 0 && RTALL % RS == 0 && 4 % RS == 0, "whole row tiles");
+    constexpr int NPX = (4 / RS) * TT * 16, LDO = COUT + 8; /* pixels per workgroup, padded LDS row */
+    __shared__ __attribute__((aligned(16))) f16 otile[NPX * LDO];
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -157,19 +162,25 @@ __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) 
     const int rt0 = (wave % RS) * RT;
     f4 acc[RT][TT];
     codec_gemm<Src, RTALL, RT, TT>(src, a.w, a.b, px, g, lane, rt0, acc);
-    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+    const int pl0 = (wave / RS) * TT * 16; /* this wave's first pixel in the workgroup's block */
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        if (!px[t].valid) continue;
-        uint16_t* row = out + ((int64_t)px[t].y * a.out_w + px[t].x) * COUT + 16 * rt0 + 4 * g;
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f4 v = acc[r][t];
             /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
-            *reinterpret_cast<h4*>(row + 16 * r) = cvt_h4(v);
+            *reinterpret_cast<h4*>(otile + (pl0 + 16 * t + l16) * LDO + 16 * (rt0 + r) + 4 * g) = cvt_h4(v);
         }
+    __syncthreads();
+    const int64_t p0 = (int64_t)blockIdx.x * NPX, npix = (int64_t)a.out_w * a.out_h;
+    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+    constexpr int CPP = COUT / 8; /* 16-byte chunks per pixel */
+    for (int q = threadIdx.x; q < NPX * CPP; q += 256) {
+        const int pl = q / CPP, c8 = (q % CPP) * 8;
+        if (p0 + pl < npix)
+            *reinterpret_cast<h8*>(out + (p0 + pl) * COUT + c8) = *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
     }
 }
 
