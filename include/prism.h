@@ -87,8 +87,9 @@ typedef struct prism_attn_push {
  * aux layout: assignment [batch*n_tokens] int32 (expert id per token),
  * counts [n_experts] (tokens per expert), and perm [n_experts][batch*n_tokens]
  * (token indices bucketed by expert: the counting sort's output; the order
- * inside a bucket is unspecified). The launch clears counts itself (a fill
- * kernel, then the router kernel), so nothing is required of them on entry. */
+ * inside a bucket is unspecified). The call writes the counts itself (the
+ * router kernel counts into a row of the context's own, then a one-workgroup
+ * launch copies the totals), so nothing is required of them on entry. */
 typedef struct prism_router_push {
     int32_t n_tokens, dim, n_experts;
     int64_t router_w, router_b;
