@@ -200,7 +200,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
                 const h4 u = cvt_h4(acc[r][t]); /* r16(W1 hn + b1) */
                 f4 gl;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gl[i] = gelu_tanh((float)u[i]);
+                for (int i = 0; i < 4; ++i) gl[i] = gelu_tanh_h(u[i]);
                 *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = cvt_h4(gl);
                 acc[r][t] = bb; /* GEMM2 starts at b2 */
             }
