@@ -6,7 +6,7 @@
  * Weights arrive in the reference's layouts (row-major [out][in]; conv
  * columns k = ic*9 + ky*3 + kx) and are repacked once into MFMA A-fragment
  * order: the stride-2 convs with columns reordered to k = tap*Cin + ic (the
- * kernels read NHWC taps), the input conv with its 81 columns padded to 96,
+ * kernels read NHWC taps), the input conv with its 81 columns as 9 taps x 16,
  * the output conv with rows padded to 16 and columns permuted to the
  * accumulator-lane order its fused kernel feeds it in. Biases become fp32.
  */
@@ -166,8 +166,11 @@ extern "C" int prism_load_codec(prism_ctx* c, const void* blob, size_t bytes, co
 
     std::vector<uint16_t> packed[8];
     const auto id = [](int j) { return j; };
-    /* enc0: k = ic*9 + tap as stored, 81 columns padded to 96 */
-    pack_mapped(w + o->enc0_w, 32, 81, 32, 96, [](int j) { return j < 81 ? j : -1; }, packed[0]);
+    /* enc0: packed column tap*16 + ic (9 taps x 16, 160 columns; ic >= 9 and
+     * tap 9 are zero) <- stored column ic*9 + tap */
+    pack_mapped(w + o->enc0_w, 32, 81, 32, 160,
+                [](int j) { const int tap = j / 16, ic = j % 16; return tap < 9 && ic < 9 ? ic * 9 + tap : -1; },
+                packed[0]);
     /* enc1..3: packed column tap*Cin + ic <- stored column ic*9 + tap */
     const int cins[3] = {32, 64, 128}, couts[3] = {64, 128, 128};
     const int64_t encw[3] = {o->enc1_w, o->enc2_w, o->enc3_w};

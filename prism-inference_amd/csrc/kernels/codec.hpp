@@ -232,14 +232,18 @@ __device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
 }
 
 /* enc0: conv3x3 9 -> 32 + ReLU straight from the CHW frame. A workgroup
- * takes a block of CODEC_ENC0_ROWS x 64 output pixels (wave w: row w, 4 tiles of 16
- * columns); the block's 9-channel input window with its 1-pixel halo is
- * first copied into LDS with coalesced row loads, and each lane then gathers
- * its B fragment elements (k = ic*9 + tap, the reference's im2col order,
- * 81 -> 96) from LDS. Grid: x = ceil(W/CODEC_ENC0_COLS) * ceil(H/CODEC_ENC0_ROWS), y = frames. */
+ * takes a block of CODEC_ENC0_ROWS x 64 output pixels (wave w: row w, 4 tiles
+ * of 16 columns). The block's input window with its 1-pixel halo is first
+ * copied into LDS pixel-interleaved, 16 halfs per pixel (the 9 channels, then
+ * zeros), one thread per pixel; the GEMM's reduction index is then
+ * k = tap * 16 + ic (9 taps x 16, padded to 160; the host packs W's stored
+ * column ic * 9 + tap there), so a lane's 8 consecutive k of a k-step are
+ * 8 channels of one tap: one 16-byte LDS read per B fragment. Grid: x =
+ * ceil(W/CODEC_ENC0_COLS) * ceil(H/CODEC_ENC0_ROWS), y = frames. */
 __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
-    constexpr int IR = CODEC_ENC0_ROWS + 2, IC = CODEC_ENC0_COLS + 2, CH = 9, TT = CODEC_ENC0_COLS / 16;
-    __shared__ f16 s_in[CH * IR * IC];
+    constexpr int IR = CODEC_ENC0_ROWS + 2, IC = CODEC_ENC0_COLS + 2, CH = 9, CP = 16, KS = 5,
+                  TT = CODEC_ENC0_COLS / 16;
+    __shared__ __attribute__((aligned(16))) f16 s_in[IR * IC * CP];
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -248,25 +252,20 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
     const int by0 = (blockIdx.x / bxn) * CODEC_ENC0_ROWS, bx0 = (blockIdx.x % bxn) * CODEC_ENC0_COLS;
     const f16* frame = reinterpret_cast<const f16*>(a.in) + (int64_t)blockIdx.y * a.in_frame;
     const int64_t plane = (int64_t)W * H;
-    for (int i = threadIdx.x; i < CH * IR * IC; i += 256) {
-        const int c = i / (IR * IC), rem = i - c * (IR * IC), r = rem / IC, x = rem - r * IC;
+    for (int px = threadIdx.x; px < IR * IC; px += 256) {
+        const int r = px / IC, x = px - r * IC;
         const int gy = by0 - 1 + r, gx = bx0 - 1 + x;
         const bool ok = gy >= 0 && gy < H && gx >= 0 && gx < W;
-        const f16 v = frame[ok ? c * plane + (int64_t)gy * W + gx : 0];
-        s_in[i] = ok ? v : (f16)0.f;
+        const f16* src = frame + (ok ? (int64_t)gy * W + gx : 0);
+        h8 lo, hi = {};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) lo[c] = ok ? src[c * plane] : (f16)0.f;
+        hi[0] = ok ? src[8 * plane] : (f16)0.f;
+        *reinterpret_cast<h8*>(s_in + px * CP) = lo;
+        *reinterpret_cast<h8*>(s_in + px * CP + 8) = hi;
     }
-    /* this lane's 24 (k-step, element) gather offsets: channel, tap row and column */
-    int off[3][8];
-#pragma unroll
-    for (int ks = 0; ks < 3; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int k = 32 * ks + 8 * g + j;
-            const int ic = k / 9, tap = k - 9 * ic;
-            off[ks][j] = k < 81 ? ic * (IR * IC) + (tap / 3) * IC + tap % 3 : -1;
-        }
     __syncthreads();
-    const FragSrc wsrc(a.w, 2u * 3u * 1024u);
+    const FragSrc wsrc(a.w, 2u * KS * 1024u);
     f4 acc[2][TT];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -275,15 +274,19 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = bb;
     }
-    const int base = wave * IC + l16; /* output row `wave`, column 16t + l16 of the block */
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-        const h8 w0 = wsrc.load(0 * 3 + ks, lane * 16), w1 = wsrc.load(1 * 3 + ks, lane * 16);
+    for (int ks = 0; ks < KS; ++ks) {
+        const h8 w0 = wsrc.load(0 * KS + ks, lane * 16), w1 = wsrc.load(1 * KS + ks, lane * 16);
+        /* k = 32 ks + 8 g + j = tap * 16 + 8 (g & 1) + j; tap 9 (the upper half
+         * of the last k-step, lane groups 2 and 3) is padding: its operand is
+         * zero, read from a clamped in-window address (no divergent branch
+         * around the MFMAs) */
+        const int tap = 2 * ks + (g >> 1), tc = tap < CH ? tap : CH - 1;
+        const int ky = tc / 3, kx = tc - 3 * ky;
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
-            h8 b;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) b[j] = off[ks][j] >= 0 ? s_in[off[ks][j] + base + 16 * t] : (f16)0.f;
+            h8 b = *reinterpret_cast<const h8*>(s_in + ((wave + ky) * IC + 16 * t + l16 + kx) * CP + 8 * (g & 1));
+            if (tap >= CH) b = h8{};
             acc[0][t] = mfma_16x16x32(w0, b, acc[0][t]);
             acc[1][t] = mfma_16x16x32(w1, b, acc[1][t]);
         }
