@@ -127,7 +127,7 @@ typedef struct CodecArgs {
 #define CODEC_ENC0_ROWS 4
 #define CODEC_ENC0_COLS 64
 #define CODEC_TT_ENC2 1
-#define CODEC_TT_ENC3 1
+#define CODEC_TT_ENC3 2
 #define CODEC_TT_DEC3 2
 #define CODEC_TT_DEC2 4
 #define CODEC_TT_DEC1 4
