@@ -44,6 +44,10 @@ static constexpr int CHAIN_COUNT_STRIDE = 64;
 static constexpr int CHAIN_SPLIT = 2;
 static constexpr int CHAIN_SPLIT_FRAMES = 2;
 static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
+/* d256 expert launches of at least this many 128-token tiles (two per CU)
+ * use the 128-token kernel: each streamed weight fragment then feeds twice
+ * the tokens. Smaller grids keep 64-token tiles (8 waves below 512 tiles). */
+static constexpr int EXPERT_WIDE_MIN_TILES = 512;
 
 enum ChainMode { CHAIN_BLOCKS = 0, CHAIN_ADAPTED = 1, CHAIN_E2E = 2 };
 
@@ -53,6 +57,7 @@ struct prism_ctx {
     hipFunction_t f_attn[2][2][5] = {}; /* [d128, d256][4 waves, 8 waves][routed: padded experts / 16] */
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
+    hipFunction_t f_expert_wide = nullptr; /* d256, 128-token tiles */
     hipFunction_t f_zero = nullptr;
     hipFunction_t f_take = nullptr;
     hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */

@@ -95,6 +95,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
         {&c->f_expert[0][0], "prism_expert_d128_bm64"},  {&c->f_expert[1][0], "prism_expert_d256_bm64"},
         {&c->f_expert[0][1], "prism_expert_d128_bm64_w8"}, {&c->f_expert[1][1], "prism_expert_d256_bm64_w8"},
+        {&c->f_expert_wide, "prism_expert_d256_bm128"},
         {&c->f_zero, "prism_zero_i32"}, {&c->f_take, "prism_take_counts"},
         {&c->f_proj[0][0], "prism_project_up_d128"},   {&c->f_proj[0][1], "prism_project_down_d128"},
         {&c->f_proj[1][0], "prism_project_up_d256"},   {&c->f_proj[1][1], "prism_project_down_d256"},
@@ -547,9 +548,12 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     a.n_experts = N;
     a.cap = (int32_t)n;
     a.count_stride = count_stride;
-    const int64_t bm = 64;
-    int64_t tiles = (n + bm - 1) / bm + (counts ? N : 0);
-    tiles = (tiles + 7) / 8 * 8;
+    /* tiles: the worst case of ceil(n / bm) + one partial tile per expert,
+     * a multiple of 8 (the kernels' XCD-major tile order) */
+    auto tiles_of = [&](int64_t bm) { return ((n + bm - 1) / bm + (counts ? N : 0) + 7) / 8 * 8; };
+    if (D == 256 && !dn && tiles_of(128) >= EXPERT_WIDE_MIN_TILES)
+        return launch(c, c->f_expert_wide, (unsigned)tiles_of(128), a, s, 256u);
+    const int64_t tiles = tiles_of(64);
     /* fewer tiles than two per CU: 8 waves per tile halve each wave's weight stream */
     const int w8 = tiles < 512 ? 1 : 0;
     return launch(c, c->f_expert[dim_index(D)][w8], (unsigned)tiles, a, s, w8 ? 512u : 256u);

@@ -157,6 +157,7 @@ __device__ __forceinline__ T opaque(T v) {
 
 /* fp16 a + b with one rounding: the reference's fp16 residual add. */
 __device__ __forceinline__ h4 add_f16x4(h4 a, h4 b) { return opaque(a) + opaque(b); }
+__device__ __forceinline__ h8 add_f16x8(h8 a, h8 b) { return opaque(a) + opaque(b); }
 
 /* Packed conversion of 4 fp32 values to fp16 (round to nearest even). */
 __device__ __forceinline__ h4 cvt_h4(f4 v) {

@@ -55,30 +55,12 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
     }
 }
 
-template <int DIM, int BM, int NW>
-__device__ __forceinline__ void expert_body(const ExpertArgs& a) {
-    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    constexpr int NT = 64 * NW;   /* threads                          */
-    constexpr int KS = DIM / 32;
-    constexpr int LDS = DIM + 8;
-    constexpr int TT = BM / 16;   /* token tiles per workgroup        */
-    constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave */
-    constexpr int LPS = DIM / 16; /* LN lanes per row                 */
-    constexpr int RPI = 64 / LPS; /* LN rows per wave iteration       */
-    static_assert(RT >= 1 && BM % (NW * RPI) == 0, "tile shape");
-
-    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, then GELU output */
-    __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
-    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
-    __shared__ int tok[BM];
-    __shared__ int sh_e, sh_row0, sh_rows;
-
-    const int lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l16 = lane & 15;
-    const int g = lane >> 4;
-
-    /* ---- schedule ------------------------------------------------------ */
+/* Tile scheduler (see the file comment): wave 0 finds this workgroup's
+ * (expert, first row, row count), or expert -1 past the last tile; the other
+ * waves stage the LayerNorm parameters meanwhile. The caller synchronises. */
+template <int DIM, int BM, int NT>
+__device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, int lane, float* s_g, float* s_b,
+                                                int& sh_e, int& sh_row0, int& sh_rows) {
     const int per_xcd = gridDim.x / 8;
     const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (wave == 0) {
@@ -112,6 +94,52 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             s_b[i] = a.ln_b[i];
         }
     }
+}
+
+/* Stages expert e's biases and the tile's token ids (-1 past the segment's
+ * end, and for a bucket entry that names no token). The caller synchronises. */
+template <int DIM, int BM, int NT>
+__device__ __forceinline__ void expert_stage_tile(const ExpertArgs& a, int e, int row0, int rows, float* s_b1,
+                                                  float* s_b2, int* tok) {
+    for (int i = threadIdx.x; i < DIM; i += NT) {
+        s_b1[i] = a.b1[(int64_t)e * DIM + i];
+        s_b2[i] = a.b2[(int64_t)e * DIM + i];
+    }
+    for (int r = threadIdx.x; r < BM; r += NT) {
+        int t = -1;
+        if (r < rows) {
+            t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
+            if (t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
+        }
+        tok[r] = t;
+    }
+}
+
+template <int DIM, int BM, int NW>
+__device__ __forceinline__ void expert_body(const ExpertArgs& a) {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int NT = 64 * NW;   /* threads                          */
+    constexpr int KS = DIM / 32;
+    constexpr int LDS = DIM + 8;
+    constexpr int TT = BM / 16;   /* token tiles per workgroup        */
+    constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave */
+    constexpr int LPS = DIM / 16; /* LN lanes per row                 */
+    constexpr int RPI = 64 / LPS; /* LN rows per wave iteration       */
+    static_assert(RT >= 1 && BM % (NW * RPI) == 0, "tile shape");
+
+    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, then GELU output */
+    __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
+    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
+    __shared__ int tok[BM];
+    __shared__ int sh_e, sh_row0, sh_rows;
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15;
+    const int g = lane >> 4;
+
+    /* ---- schedule ------------------------------------------------------ */
+    expert_schedule<DIM, BM, NT>(a, wave, lane, s_g, s_b, sh_e, sh_row0, sh_rows);
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_e);
 
@@ -121,18 +149,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
         const int loff = lane * 16;
 
-        for (int i = threadIdx.x; i < DIM; i += NT) {
-            s_b1[i] = a.b1[(int64_t)e * DIM + i];
-            s_b2[i] = a.b2[(int64_t)e * DIM + i];
-        }
-        for (int r = threadIdx.x; r < BM; r += NT) {
-            int t = -1;
-            if (r < rows) {
-                t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
-                if (t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
-            }
-            tok[r] = t;
-        }
+        expert_stage_tile<DIM, BM, NT>(a, e, row0, rows, s_b1, s_b2, tok);
         __syncthreads();
 
         /* the gathered rows' loads go out first, then every W1 fragment of
@@ -287,6 +304,194 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 
 }
 
+/* GELU of one accumulator: u = r16(acc), g = r16(GELU-tanh(u)). */
+__device__ __forceinline__ h4 expert_gelu4(const f4& acc) {
+    const h4 u = cvt_h4(acc);
+    f4 gl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gl[i] = gelu_tanh_h(u[i]);
+    return cvt_h4(gl);
+}
+
+/* One GEMM of a 128-token tile: acc[r][t] += W(row tile r) * tile^T over the
+ * KS k-steps. Weight fragment p = P0 + ks*RT + r of the wave's stream sits in
+ * ring[p % PF] and is replaced by fragment p + PF as soon as it has fed its
+ * last MFMA. Token tiles go in two halves whose LDS operand reads are double-
+ * buffered against each other (half B's reads go out before half A's MFMAs,
+ * the next k-step's half A before half B's); every operand fragment feeds RT
+ * MFMAs. */
+template <int KS, int LDS, int RT, int TT, int PF, int P0, int NF, class Frag>
+__device__ __forceinline__ void expert_wide_gemm(f4 (&acc)[RT][TT], h8 (&ring)[PF], const f16* tile, int l16, int g,
+                                                 Frag&& frag) {
+    constexpr int TH = TT / 2;
+    h8 xa[TH], xb[TH];
+#pragma unroll
+    for (int t = 0; t < TH; ++t) xa[t] = *reinterpret_cast<const h8*>(tile + (16 * t + l16) * LDS + 8 * g);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int t = 0; t < TH; ++t)
+            xb[t] = *reinterpret_cast<const h8*>(tile + (16 * (TH + t) + l16) * LDS + 32 * ks + 8 * g);
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int t = 0; t < TH; ++t) acc[r][t] = mfma_16x16x32(ring[(P0 + ks * RT + r) % PF], xa[t], acc[r][t]);
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < TH; ++t)
+                xa[t] = *reinterpret_cast<const h8*>(tile + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int p = P0 + ks * RT + r;
+#pragma unroll
+            for (int t = 0; t < TH; ++t) acc[r][TH + t] = mfma_16x16x32(ring[p % PF], xb[t], acc[r][TH + t]);
+            if (p + PF < NF) ring[p % PF] = frag(p + PF);
+        }
+        sched_fence();
+    }
+}
+
+/*
+ * 128-token tiles on 4 waves (two workgroups per CU), for the large grids of
+ * batched launches. Every weight fragment a wave streams feeds 8 token tiles
+ * instead of 4, which halves the weight bytes per FLOP through the vector
+ * memory pipe, and each token's share of a tile's serial prologue (counts,
+ * bucket entries, row gather) halves too, while every LDS operand fragment
+ * still feeds 4 MFMAs (one per row tile of the wave). The wave's weights
+ * (W1's 64 rows, then W2's) stream through a ring of PF fragments, k-step-
+ * major, so W2's first fragments are in flight during the GELU. The LDS holds
+ * one 128-row tile (LN2 output, then GELU output, then y) and not the
+ * residual: the tile's input rows (L2-resident since the gather) are read
+ * again as GEMM2 ends and added to y as whole rows, 16 bytes per lane.
+ * Per output element the arithmetic and its order are those of expert_body
+ * (bias in the accumulator, k-steps in order, the same rounding points), so
+ * the results are bit-identical to the 64-token kernels.
+ */
+template <int DIM, int PF>
+__device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
+    constexpr int BM = 128, NW = 4, NT = 64 * NW;
+    constexpr int KS = DIM / 32;
+    constexpr int LDS = DIM + 8;
+    constexpr int TT = BM / 16;       /* token tiles                   */
+    constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave  */
+    constexpr int NF = 2 * RT * KS;   /* fragments in the wave's stream */
+    constexpr int LPS = DIM / 16;     /* LN lanes per row              */
+    constexpr int RPI = 64 / LPS;     /* LN rows per wave iteration    */
+    constexpr int IT = BM / NW / RPI;
+    static_assert(RT >= 1 && BM % (NW * RPI) == 0 && PF % RT == 0 && PF <= NF, "tile shape");
+
+    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, GELU output, y */
+    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
+    __shared__ int tok[BM];
+    __shared__ int sh_e, sh_row0, sh_rows;
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15;
+    const int g = lane >> 4;
+
+    expert_schedule<DIM, BM, NT>(a, wave, lane, s_g, s_b, sh_e, sh_row0, sh_rows);
+    __syncthreads();
+    const int e = __builtin_amdgcn_readfirstlane(sh_e);
+    if (e < 0) return;
+
+    const FragSrc w1(a.w1 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
+    const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
+    const int loff = lane * 16;
+    /* fragment p of the stream: W1 then W2, k-step-major, the wave's RT row tiles */
+    auto frag = [&](int p) -> h8 {
+        const int q = p % (RT * KS), ks = q / RT, r = q % RT;
+        return (p < RT * KS ? w1 : w2).load((wave * RT + r) * KS + ks, loff);
+    };
+    expert_stage_tile<DIM, BM, NT>(a, e, sh_row0, sh_rows, s_b1, s_b2, tok);
+    __syncthreads();
+
+    /* rows first, then the ring's first fragments; LN2 runs while they arrive */
+    RowChunk rc[IT];
+    int rt_tok[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
+        rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM, rt_tok[it] >= 0);
+    }
+    h8 ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) ring[p] = frag(p);
+    sched_fence();
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int r = wave * (BM / NW) + it * RPI + lane / LPS;
+        ln_store<DIM>(rc[it], rt_tok[it] >= 0, s_g, s_b, xs + r * LDS, nullptr);
+    }
+    __syncthreads();
+
+    f4 acc[RT][TT];
+    h4 res[RT][TT];
+    /* ---- GEMM1 + GELU ------------------------------------------------- */
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int ch = (wave * RT + r) * 16 + 4 * g;
+        const f4 bb = {s_b1[ch], s_b1[ch + 1], s_b1[ch + 2], s_b1[ch + 3]};
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+    }
+    expert_wide_gemm<KS, LDS, RT, TT, PF, 0, NF>(acc, ring, xs, l16, g, frag);
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) res[r][t] = expert_gelu4(acc[r][t]);
+    __syncthreads(); /* every wave is done reading the LN tile */
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g) = res[r][t];
+    __syncthreads();
+    /* ---- GEMM2 -------------------------------------------------------- */
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int ch = (wave * RT + r) * 16 + 4 * g;
+        const f4 bb = {s_b2[ch], s_b2[ch + 1], s_b2[ch + 2], s_b2[ch + 3]};
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+    }
+    expert_wide_gemm<KS, LDS, RT, TT, PF, RT * KS, NF>(acc, ring, xs, l16, g, frag);
+    /* the residual rows (L2-resident since the gather) are requested now, so
+     * their latency hides behind the y tile's conversion and barriers */
+    constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
+    constexpr int RPS = 64 / CPR; /* rows per wave access   */
+    constexpr int NI = BM / NW / RPS;
+    static_assert(64 % CPR == 0 && (BM / NW) % RPS == 0, "row shape");
+    const int c8 = (lane % CPR) * 8;
+    h8 hx[NI];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+        const int tk = tok[wave * (BM / NW) + it * RPS + lane / CPR];
+        hx[it] = tk >= 0 ? *reinterpret_cast<const h8*>(a.in + (int64_t)tk * DIM + c8) : h8{};
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) res[r][t] = cvt_h4(acc[r][t]); /* y = r16(W2 g + b2) */
+    __syncthreads(); /* every wave is done reading the GELU tile */
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g) = res[r][t];
+    __syncthreads(); /* y tile complete */
+    /* ---- out = y + h in fp16 (one rounding), whole rows --------------- */
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+        const int r = wave * (BM / NW) + it * RPS + lane / CPR;
+        const int tk = tok[r];
+        if (tk >= 0)
+            *reinterpret_cast<h8*>(a.out + (int64_t)tk * DIM + c8) =
+                add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]);
+    }
+}
+
 /* 4 waves (2 workgroups per CU) for large grids; 8 waves (each streaming half
  * as many weight rows) when tiles are scarcer than CUs. */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm64(ExpertArgs a) {
@@ -300,4 +505,9 @@ extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d256_bm64_w8(E
 }
 extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d128_bm64_w8(ExpertArgs a) {
     expert_body<128, 64, 8>(a);
+}
+/* 128-token tiles, 4 waves, 2 workgroups per CU: the large grids of batched
+ * launches (no fused down-projection) */
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm128(ExpertArgs a) {
+    expert_body_wide<256, 12>(a);
 }

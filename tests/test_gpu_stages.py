@@ -164,6 +164,59 @@ def test_dense_ffn_stage(hip, engine, device_arena, name, H, W, batch):
     assert mx <= MAX_ABS and mean <= MEAN_ABS
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["moe64", "std256"])
+def test_experts_wide_tiles(hip, engine, device_arena, name):
+    """8 frames at 68x120 (65,280 tokens) give the d256 expert launch 512 or
+    more 128-token tiles, so it runs the 128-token kernel; one frame alone runs
+    the 64-token kernel (8 waves). Each token's routing and output must be
+    bit-identical between the two (same arithmetic per token), and the batch's
+    outputs must match the oracle, teacher-forced with the GPU's routing, on
+    a sample of tokens (the expert stage acts per token)."""
+    cfg = P.CONFIGS[name]
+    H, W, B = 68, 120, 8
+    desc, blob, offs, w = make_model(cfg, 1, H, W)
+    engine.load_weights(desc, blob, offs)
+    T, d, N = H * W, cfg.dim, cfg.n_experts
+    routed = N > 1
+    h_bits = P.synth_features(cfg, batch=B, H=H, W=W, seed=5).reshape(B * T, d)
+
+    def run(frames, first):
+        n = frames * T
+        feats = device_arena(2 * n * d * 2)
+        hip.upload(feats.ptr, h_bits[first * T:(first + frames) * T])
+        print(f"[wide] {name} {frames} frame(s) from {first}", flush=True)
+        if routed:
+            aux = device_arena(P.aux_elems(N, n) * 4)
+            rc = engine.router(engine.router_push(0, T, 0, 0, n, n + N), feats.ptr, aux.ptr, frames)
+            assert rc == 0, engine.error()
+            rc = engine.experts(engine.expert_push(0, T, 0, n * d, 0, n, n + N), feats.ptr, aux.ptr, frames)
+            assert rc == 0, engine.error()
+        else:
+            rc = engine.experts(engine.expert_push(0, T, 0, n * d), feats.ptr, None, frames)
+            assert rc == 0, engine.error()
+        hip.sync()
+        y = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2).reshape(n, d)
+        assign = hip.download(np.empty(n, np.int32), aux.ptr) if routed else np.zeros(n, np.int32)
+        return y, assign
+
+    y, assign = run(B, 0)
+    y1, assign1 = run(1, 3)
+    assert (assign1 == assign[3 * T:4 * T]).all(), "routing of frame 3 differs"
+    diff = int((y1 != y[3 * T:4 * T]).sum())
+    assert diff == 0, f"{diff} output values of frame 3 differ between the 128- and 64-token kernels"
+
+    rng = np.random.default_rng(0)
+    idx = np.sort(np.concatenate([np.arange(256), rng.choice(B * T, 3840, replace=False)]))
+    idx = np.unique(idx)
+    ref = O.expert_stage(ocfg(cfg, 1, len(idx), 1), w, offs[0], f16(h_bits[idx]),
+                         assign[idx] if routed else None)
+    mx, mean = errors(f16(y[idx]), ref)
+    print(f"[wide] {name}: {len(idx)} sampled tokens, max {mx:.3g} mean {mean:.3g}; "
+          f"load max share {np.bincount(assign, minlength=N).max() / (B * T):.3f}")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
 FUSED_EXTRA = {
     "moe40": P.Config("moe40", 256, 2, 8, 32, 40, 68, 120, 1, P.ROUTE_UNIFORM),
     "moe24d128": P.Config("moe24d128", 128, 2, 8, 16, 24, 68, 120, 1, P.ROUTE_ZIPF),
