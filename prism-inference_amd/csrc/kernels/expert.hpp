@@ -32,6 +32,12 @@
  * the tokens' HWC positions as whole 512-byte rows, 16 bytes per lane (fused
  * unpermute; one store instruction covers two rows instead of 16 tokens x
  * 32 bytes).
+ *
+ * Two tile sizes: expert_body (64 tokens, 4 or 8 waves; the weight-streaming
+ * scheme above) and expert_body_wide (128 tokens, 4 waves, d256, for large
+ * grids: a weight ring instead of per-pass registers, the residual read
+ * again instead of kept in LDS; see its comment). Both share the scheduler
+ * and give bit-identical results.
  */
 #pragma once
 #include "common.hpp"
