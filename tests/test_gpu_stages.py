@@ -165,16 +165,19 @@ def test_dense_ffn_stage(hip, engine, device_arena, name, H, W, batch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["moe64", "std256"])
-def test_experts_wide_tiles(hip, engine, device_arena, name):
-    """8 frames at 68x120 (65,280 tokens) give the d256 expert launch 512 or
+@pytest.mark.parametrize("name,H,W,B", [
+    ("moe64", 68, 120, 8),     # Zipf(1.1) load
+    ("std256", 68, 120, 8),    # dense FFN (expert 0, no buckets)
+    ("moe32", 135, 240, 4),    # adversarial: half of the tokens on one expert (~500 of its tiles)
+])
+def test_experts_wide_tiles(hip, engine, device_arena, name, H, W, B):
+    """A batch of 65,280 or more tokens gives the d256 expert launch 512 or
     more 128-token tiles, so it runs the 128-token kernel; one frame alone runs
-    the 64-token kernel (8 waves). Each token's routing and output must be
-    bit-identical between the two (same arithmetic per token), and the batch's
-    outputs must match the oracle, teacher-forced with the GPU's routing, on
-    a sample of tokens (the expert stage acts per token)."""
+    a 64-token kernel. Each token's routing and output must be bit-identical
+    between the two (same arithmetic per token), and the batch's outputs must
+    match the oracle, teacher-forced with the GPU's routing, on a sample of
+    tokens (the expert stage acts per token)."""
     cfg = P.CONFIGS[name]
-    H, W, B = 68, 120, 8
     desc, blob, offs, w = make_model(cfg, 1, H, W)
     engine.load_weights(desc, blob, offs)
     T, d, N = H * W, cfg.dim, cfg.n_experts
