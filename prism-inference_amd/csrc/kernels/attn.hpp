@@ -53,7 +53,11 @@ struct AttnShape {
     static constexpr int ORT = DIM / 16 / NW;      /* out-proj row tiles per wave    */
     static constexpr int OUTF = KS * ORT;          /* out-proj fragments             */
     static constexpr int RBASE = HPW * HEADF + OUTF; /* sequence length, no routing  */
-    static constexpr int TOTAL = RBASE + NPT * KS;   /* routing waves add W_r        */
+    /* 8 waves, even NPT: waves w and w+4 route the same 16 tokens, each over
+     * half of the expert row tiles (RPT of them) */
+    static constexpr bool RSPLIT = NW == 8 && NPT > 0 && NPT % 2 == 0;
+    static constexpr int RPT = RSPLIT ? NPT / 2 : NPT;
+    static constexpr int TOTAL = RBASE + RPT * KS;   /* routing waves add W_r        */
     static constexpr int PF = 2 * FPK;             /* ring depth (2 k-steps ahead)   */
     static constexpr int LDS = DIM + 8;            /* padded LDS row, halfs          */
 };
@@ -80,8 +84,9 @@ __device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, 
         return wo.load((wave * S::ORT + r) * S::KS + ks, loff);
     }
     const int q = p - S::RBASE;
-    const int ks = q / (NPT > 0 ? NPT : 1), rt = q % (NPT > 0 ? NPT : 1);
-    return wr.load(rt * S::KS + ks, loff);
+    constexpr int R = S::RPT > 0 ? S::RPT : 1;
+    const int rt0 = S::RSPLIT && wave >= 4 ? S::RPT : 0; /* the upper half's row tiles */
+    return wr.load((rt0 + q % R) * S::KS + q / R, loff);
 }
 
 template <int DIM, int HD, int NW, int NPT>
@@ -132,7 +137,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     const FragSrc src_r(NPT > 0 ? a.wr : a.wo, NPT > 0 ? 16u * NPT * DIM * 2u : 0u);
     const int loff = lane * 16;
     /* waves 0-3 route tiles 0-3 of the window; only they stream W_r */
-    const bool routes = NPT > 0 && wave < 4;
+    const bool routes = NPT > 0 && (S::RSPLIT || wave < 4);
     const int total = routes ? S::TOTAL : S::RBASE;
 
     /* ---- 1. LN1 --------------------------------------------------------
@@ -460,19 +465,49 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
 
     /* ---- 5. fused routing (moe_router.comp.glsl:24-52 + counting sort) -- */
     if constexpr (NPT > 0) {
-        if (routes) {    /* wave w: tokens 16w..16w+15, all experts */
+        auto rfrag = [&](int rt, int ks) {
+            const int p = S::RBASE + ks * S::RPT + rt;
+            const h8 w = ring[p % PF];
+            if (p + PF < S::TOTAL)
+                ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
+            return w;
+        };
+        if constexpr (S::RSPLIT) {
+            /* waves w and w+4: tokens 16(w%4)..+15, expert row tiles [0, RPT) and
+             * [RPT, NPT); the upper half's best goes through LDS (xs is free) and
+             * is merged in row-tile order, which keeps the first maximum */
+            float* const r_pv = reinterpret_cast<float*>(xs);
+            int* const r_pe = reinterpret_cast<int*>(xs) + 64;
+            const int sl = 16 * (wave & 3) + l16;
+            h8 cur[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
+            float bv;
+            int be;
+            route_partial<DIM, S::RPT>(cur, s_g2, s_b2, s_br, g, wave >= 4 ? S::RPT : 0, rfrag, bv, be);
+            if (wave >= 4 && g == 0) {
+                r_pv[sl] = bv;
+                r_pe[sl] = be;
+            }
+            __syncthreads();
+            if (wave < 4) {
+                float v;
+                int e;
+                route_pick(bv, be, r_pv[sl], r_pe[sl], v, e);
+                if (e >= a.n_experts || e < 0) e = 0; /* non-finite logits */
+                const int sy = wy * 8 + (sl >> 3), sx = wxx * 8 + (sl & 7);
+                if (g == 0) {
+                    r_e[sl] = e;
+                    r_rank[sl] = (sy < a.H && sx < a.W) ? atomicAdd(&r_hist[e], 1) : 0;
+                }
+            }
+        } else if (routes) { /* wave w: tokens 16w..16w+15, all experts */
             const int sl = 16 * wave + l16;
             const int sy = wy * 8 + (sl >> 3), sx = wxx * 8 + (sl & 7);
             h8 cur[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
-            const int e = route_token<DIM, NPT>(cur, s_g2, s_b2, s_br, g, a.n_experts, [&](int rt, int ks) {
-                const int p = S::RBASE + ks * NPT + rt;
-                const h8 w = ring[p % PF];
-                if (p + PF < S::TOTAL)
-                    ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
-                return w;
-            });
+            const int e = route_token<DIM, NPT>(cur, s_g2, s_b2, s_br, g, a.n_experts, rfrag);
             if (g == 0) {
                 r_e[sl] = e;
                 r_rank[sl] = (sy < a.H && sx < a.W) ? atomicAdd(&r_hist[e], 1) : 0;

@@ -82,29 +82,44 @@ __device__ __forceinline__ void route_combine_groups(float& best_v, int& best_e)
     route_pick(av, ae, bv, be, best_v, best_e);
 }
 
-/* frag(rt, ks) returns router fragment (row tile rt, k-step ks) of the packed
- * W_r. s_br holds 16*NPT biases with -inf past the real experts. Returns the
- * token's expert in all 4 lane groups of its column. */
-template <int DIM, int NPT, class Frag>
-__device__ __forceinline__ int route_token(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
-                                           const float* s_br, int g, int n_experts, Frag&& frag) {
+/* The best (fp16 logit, expert) of row tiles rt0 .. rt0+NR-1 for the token of
+ * this lane's column, the same in all 4 lane groups. frag(r, ks) returns the
+ * packed W_r fragment of row tile rt0 + r, k-step ks. s_br holds 16*NPT
+ * biases with -inf past the real experts. Larger logit wins, ties go to the
+ * lower id, so the best of consecutive ranges merged in range order with
+ * route_pick equals the best of their union. */
+template <int DIM, int NR, class Frag>
+__device__ __forceinline__ void route_partial(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
+                                              const float* s_br, int g, int rt0, Frag&& frag, float& best_v,
+                                              int& best_e) {
     constexpr int KS = DIM / 32;
     h8 hn[KS];
     route_ln<DIM>(cur, s_g, s_b, g, hn);
-    f4 acc[NPT]; /* starts at the router bias */
+    f4 acc[NR]; /* starts at the router bias */
 #pragma unroll
-    for (int rt = 0; rt < NPT; ++rt)
-        acc[rt] = f4{s_br[16 * rt + 4 * g], s_br[16 * rt + 4 * g + 1], s_br[16 * rt + 4 * g + 2],
-                     s_br[16 * rt + 4 * g + 3]};
+    for (int r = 0; r < NR; ++r) {
+        const int b = 16 * (rt0 + r) + 4 * g;
+        acc[r] = f4{s_br[b], s_br[b + 1], s_br[b + 2], s_br[b + 3]};
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int rt = 0; rt < NPT; ++rt) acc[rt] = mfma_16x16x32(frag(rt, ks), hn[ks], acc[rt]);
-    float best_v = -3.0e38f;
-    int best_e = 0x7fffffff;
+        for (int r = 0; r < NR; ++r) acc[r] = mfma_16x16x32(frag(r, ks), hn[ks], acc[r]);
+    best_v = -3.0e38f;
+    best_e = 0x7fffffff;
 #pragma unroll
-    for (int rt = 0; rt < NPT; ++rt) route_tile_best(acc[rt], rt, g, best_v, best_e);
+    for (int r = 0; r < NR; ++r) route_tile_best(acc[r], rt0 + r, g, best_v, best_e);
     route_combine_groups(best_v, best_e);
+}
+
+/* The token's expert over all NPT row tiles (frag(rt, ks) as above with
+ * rt0 = 0), in all 4 lane groups of its column. */
+template <int DIM, int NPT, class Frag>
+__device__ __forceinline__ int route_token(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
+                                           const float* s_br, int g, int n_experts, Frag&& frag) {
+    float best_v;
+    int best_e;
+    route_partial<DIM, NPT>(cur, s_g, s_b, s_br, g, 0, frag, best_v, best_e);
     if (best_e >= n_experts || best_e < 0) best_e = 0; /* non-finite logits */
     return best_e;
 }
