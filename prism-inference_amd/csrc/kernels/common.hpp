@@ -101,6 +101,21 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+/* Inclusive prefix sum over the 64 lanes of a wave on DPP (no LDS crossbar):
+ * shifted adds within each row of 16 (row_shr 1, 2, 4, 8; lanes shifted in
+ * from outside the row add 0), then row 0's total into row 1 and row 2's
+ * into row 3 (row_bcast:15 on rows 1 and 3), then the total of rows 0-1 into
+ * rows 2 and 3 (row_bcast:31). */
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false); /* row_shr:1  */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false); /* row_shr:2  */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false); /* row_shr:4  */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false); /* row_shr:8  */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); /* row_bcast:15 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); /* row_bcast:31 */
+    return v;
+}
+
 /* One fragment (1 KiB, 16 B per lane) of a packed weight matrix. */
 __device__ __forceinline__ h8 load_frag(const uint16_t* packed, int frag, int lane) {
     return reinterpret_cast<const h8*>(packed)[frag * 64 + lane];

@@ -13,7 +13,8 @@
  * (i % 8) * (grid / 8) + i / 8 so that consecutive tiles of one expert land on
  * the same XCD (hardware dispatches workgroups round-robin over the 8 XCDs)
  * and share that XCD's L2 copy of the expert's weights. Wave 0 turns the
- * per-expert counts into a tile prefix sum and finds its (expert, row block);
+ * per-expert counts into a tile prefix sum (a DPP scan) and finds its
+ * (expert, row block);
  * tiles past the end do nothing.
  *
  * Weight streaming: as soon as the tokens are gathered, each wave issues
@@ -73,12 +74,7 @@ __device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, i
         if (a.counts) {
             const int c = lane < a.n_experts ? min(a.counts[lane * a.count_stride], a.cap) : 0;
             const int nt = (c + BM - 1) / BM;
-            int incl = nt;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int v = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += v;
-            }
+            const int incl = wave_incl_scan(nt);
             const int excl = incl - nt;
             const bool mine = lane < a.n_experts && L >= excl && L < incl;
             const unsigned long long bal = __ballot(mine);
