@@ -283,3 +283,64 @@ def test_attn_route_rejects_mismatched_pushes(hip, engine, device_arena):
     wrong_input = engine.router_push(0, n, 0, 0, n, n + N)
     assert engine.attn_route(pa, wrong_input, feats.ptr, aux.ptr, 1) == P.ERR_INVALID
     assert "attention output" in engine.error()
+
+
+@pytest.mark.gpu
+def test_stage_calls_reject_bad_pushes(hip, engine, device_arena):
+    """Every stage call validates its push against the loaded model before it
+    launches anything: a push naming the wrong shape, offsets that name no
+    loaded block, negative or misaligned feature offsets, a batch below 1, NULL
+    buffers, or a routed expert stage without its aux arena is refused with
+    PRISM_ERR_INVALID and a message, the features are left untouched, and the
+    context stays usable."""
+    cfg = P.CONFIGS["moe16"]
+    H, W = 9, 13
+    desc, blob, offs, w = make_model(cfg, 2, H, W)
+    engine.load_weights(desc, blob, offs)
+    n, d, N = H * W, cfg.dim, cfg.n_experts
+    feats = device_arena(2 * n * d * 2)
+    aux = device_arena(P.aux_elems(N, n) * 4)
+    x = P.synth_features(cfg, batch=1, H=H, W=W, seed=7).reshape(n, d)
+    hip.upload(feats.ptr, x)
+    hip.memset(feats.ptr + n * d * 2, 0xFF, n * d * 2)  # output region: sentinel
+
+    def changed(push, **kw):
+        q = type(push).from_buffer_copy(push)
+        for k, v in kw.items():
+            setattr(q, k, v)
+        return q
+
+    pa = engine.attn_push(0, 0, n * d, H, W)
+    pr = engine.router_push(0, n, n * d, 0, n, n + N)
+    pe = engine.expert_push(0, n, n * d, 0, 0, n, n + N)
+    bad = [
+        ("attn dim", lambda: engine.attn(changed(pa, dim=128), feats.ptr, 1)),
+        ("attn n_tokens", lambda: engine.attn(changed(pa, n_tokens=n - 1), feats.ptr, 1)),
+        ("attn qkv_w", lambda: engine.attn(changed(pa, qkv_w=pa.qkv_w + 8), feats.ptr, 1)),
+        ("attn negative input", lambda: engine.attn(changed(pa, input_offset=-8), feats.ptr, 1)),
+        ("attn misaligned output", lambda: engine.attn(changed(pa, output_offset=n * d + 1), feats.ptr, 1)),
+        ("attn batch 0", lambda: engine.attn(pa, feats.ptr, 0)),
+        ("attn NULL features", lambda: engine.attn(pa, 0, 1)),
+        ("router n_experts", lambda: engine.router(changed(pr, n_experts=N + 1), feats.ptr, aux.ptr, 1)),
+        ("router router_w", lambda: engine.router(changed(pr, router_w=pr.router_w + 8), feats.ptr, aux.ptr, 1)),
+        ("router misaligned input", lambda: engine.router(changed(pr, input_offset=n * d + 4), feats.ptr, aux.ptr, 1)),
+        ("router NULL aux", lambda: engine.router(pr, feats.ptr, 0, 1)),
+        ("experts dim", lambda: engine.experts(changed(pe, dim=128), feats.ptr, aux.ptr, 1)),
+        ("experts n_experts", lambda: engine.experts(changed(pe, n_experts=N - 1), feats.ptr, aux.ptr, 1)),
+        ("experts w1", lambda: engine.experts(changed(pe, w1=pe.w1 + 8), feats.ptr, aux.ptr, 1)),
+        ("experts routed without aux", lambda: engine.experts(pe, feats.ptr, 0, 1)),
+        ("experts negative output", lambda: engine.experts(changed(pe, output_offset=-8), feats.ptr, aux.ptr, 1)),
+        ("experts batch 0", lambda: engine.experts(pe, feats.ptr, aux.ptr, 0)),
+    ]
+    for what, call in bad:
+        rc = call()
+        assert rc == P.ERR_INVALID, f"{what}: rc {rc}"
+        assert engine.error(), what
+    hip.sync()
+    out = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2)
+    assert (out == 0xFFFF).all(), "a refused call wrote features"
+    # the context still works: the valid pushes run
+    assert engine.attn(pa, feats.ptr, 1) == 0, engine.error()
+    hip.sync()
+    out = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2)
+    assert not (out == 0xFFFF).all()
