@@ -198,3 +198,46 @@ def test_end_to_end_drift(hip, engine, device_arena, name, nb, H, W, batch):
     print(f"[e2e] {name}: max {err.max():.3g} mean {err.mean():.3g}, tokens moved > {MAX_ABS}: {moved:.4f}")
     assert err.mean() <= MEAN_ABS
     assert moved <= 0.02
+
+
+@pytest.mark.gpu
+def test_forward_rejects_bad_arguments(hip, device_arena):
+    """The chain entry points refuse, before any launch: no weights loaded
+    (PRISM_ERR_STATE), the adapted chain without adapters (PRISM_ERR_STATE),
+    NULL or misaligned buffers and a batch below 1 (PRISM_ERR_INVALID); the
+    output buffer is left untouched and the context keeps working."""
+    eng = P.Engine(0)
+    try:
+        cfg = P.CONFIGS["moe16"]
+        H, W = 9, 13
+        n, d = H * W, cfg.dim
+        dx, dy = device_arena(n * d * 2 + 64), device_arena(n * d * 2 + 64)
+        for graph in (False, True):
+            with pytest.raises(P.PrismError) as ei:
+                eng.forward(dx.ptr, dy.ptr, 1, graph=graph)
+            assert ei.value.code == P.ERR_STATE and "not loaded" in eng.error()
+        desc = cfg.desc(n_blocks=2, H=H, W=W)
+        blob, offs = P.synth_weights(desc, seed=0, routing=cfg.routing)
+        eng.load_weights(desc, blob, offs)
+        hip.upload(dx.ptr, P.synth_features(cfg, batch=1, H=H, W=W, seed=8).reshape(n, d))
+        hip.memset(dy.ptr, 0xFF, n * d * 2 + 64)
+        bad = [
+            ("NULL in", lambda g: eng.forward(0, dy.ptr, 1, graph=g), P.ERR_INVALID),
+            ("NULL out", lambda g: eng.forward(dx.ptr, 0, 1, graph=g), P.ERR_INVALID),
+            ("misaligned out", lambda g: eng.forward(dx.ptr, dy.ptr + 2, 1, graph=g), P.ERR_INVALID),
+            ("batch 0", lambda g: eng.forward(dx.ptr, dy.ptr, 0, graph=g), P.ERR_INVALID),
+            ("adapted without adapters", lambda g: eng.forward(dx.ptr, dy.ptr, 1, graph=g, adapted=True),
+             P.ERR_STATE),
+        ]
+        for what, call, code in bad:
+            for graph in (False, True):
+                with pytest.raises(P.PrismError) as ei:
+                    call(graph)
+                assert ei.value.code == code, f"{what} (graph={graph}): {ei.value.code}"
+        hip.sync()
+        assert (hip.download(np.empty(n * d + 32, np.uint16), dy.ptr) == 0xFFFF).all(), "a refused call wrote out"
+        eng.forward(dx.ptr, dy.ptr, 1, graph=True)
+        hip.sync()
+        assert not (hip.download(np.empty(n * d, np.uint16), dy.ptr) == 0xFFFF).all()
+    finally:
+        eng.close()
