@@ -83,6 +83,7 @@ EXTRA = {
     ("moe24d128", 3, 68, 120, 1),
     ("moe24d128", 2, 68, 120, 4),
     ("moe64", 2, 68, 120, 16),     # sub-chains of 8 frames: 128-token expert tiles
+    ("moe32", 2, 135, 240, 1),     # 510 windows, 8 waves, 2 router row tiles split over wave pairs
 ])
 def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch):
     """The chain routes inside the attention kernel; the stage calls run the
