@@ -220,8 +220,8 @@ class Config:
         return 2 * (qkv + attn + out + router + ffn)
 
 
-# The five workloads the build is specified on (dense baseline, standard dense,
-# MoE-16, MoE-64 headline, MoE-32 deep at 1080p-native).
+# The five workloads of the path (dense baseline, standard dense, MoE-16, the
+# MoE-64 headline, MoE-32 deep at 1080p-native): shape, block count, routing.
 CONFIGS = {
     "dense128": Config("dense128", 128, 4, 8, 16, 1, 68, 120, 1, ROUTE_RANDOM),
     "std256": Config("std256", 256, 12, 8, 32, 1, 68, 120, 1, ROUTE_RANDOM),
