@@ -216,8 +216,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the block chain on one GPU "
-              "(frames and windows shard with no exchange; see DESIGN.md). Run with --gpus 1.",
+        print(f"bench.py: --gpus {args.gpus} is not supported: the block chain runs on one GPU "
+              "(frames and windows would shard across GPUs with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 

@@ -14,8 +14,8 @@
  *    offset, row-major [out][in] (prism_moe_bench.cpp:164-172,
  *    vulkan_engine/export_weights.py:96-120).
  *  - One launch per block stage; the launch parameter structs mirror the
- *    stages' push-constant blocks field for field, plus the pre-LayerNorm
- *    offsets this build adds.
+ *    stages' push-constant blocks field for field, plus the offsets of the
+ *    pre-LayerNorm tensors (LN1 before attention, LN2 before router/experts).
  *  - Feature and aux arenas are caller-owned device buffers addressed by
  *    element offsets, as the reference's bindings 1 (fp16 features) and 2
  *    (int32 aux) are.
@@ -117,7 +117,7 @@ typedef struct prism_expert_push {
 
 /* ---- host-only helpers (no GPU needed) -------------------------------- */
 
-/* Fill offs[0..n_blocks) with the build's blob layout (the reference's bump
+/* Fill offs[0..n_blocks) with the blob layout (the reference's bump
  * allocator wa(), prism_moe_bench.cpp:164-172, repeated per block with the LN
  * tensors added) and return the blob size in elements. offs may be NULL. */
 int prism_layout(const prism_model_desc* desc, prism_block_offsets* offs,
