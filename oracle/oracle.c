@@ -1,8 +1,8 @@
 /*
  * oracle.c - fp32 CPU restatement (OpenMP) of the Prism bottleneck block chain.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the CPU baseline
- * of the bench. Nothing in the product links, loads or calls it.
+ * TEST INFRASTRUCTURE ONLY: the parity reference for the HIP path and the CPU
+ * baseline of the bench. Nothing in the product links, loads or calls it.
  *
  * Each function cites the reference lines it restates (paths relative to the
  * reference repository). The numerics contract it implements:

@@ -1,7 +1,7 @@
 /*
  * oracle.h - CPU restatement of the Prism bottleneck block chain.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY. This library is the parity oracle: tests/, the smoke
  * entry point and the bench's cpu_baseline leg may load it; the product
  * (libprism.so + prism_kernels.hsaco) never links, loads or calls it.
  *

@@ -2,7 +2,7 @@
 Prism block chain (oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke entry point and the
-bench's cpu_baseline leg, as the checker. The product never imports it.
+bench's cpu_baseline leg, as the parity oracle. The product never imports it.
 
 All arrays are float32 numpy arrays holding fp16-representable values on
 input (fp16 bits are widened with numpy's exact float16 -> float32 cast).
