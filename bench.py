@@ -173,7 +173,14 @@ def cpu_baseline(cfg, blob, offs, x_bits, budget_s, batch):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    # OpenMP threads: the environment's OMP_NUM_THREADS if set (on a shared
+    # GPU host, the CPU share that comes with one GPU), else every CPU this
+    # process may run on; the host's own CPU count is reported beside it
+    host_cpus = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_cpus
+    env = os.environ.get("OMP_NUM_THREADS", "").strip()
+    threads = int(env) if env.isdigit() and int(env) > 0 else usable
+    threads_from = f"OMP_NUM_THREADS={env}" if env.isdigit() and int(env) > 0 else "all CPUs in the affinity mask"
     O.set_threads(threads)
     w = O.f16bits_to_f32(blob)
     n = cfg.H * cfg.W
@@ -187,7 +194,8 @@ def cpu_baseline(cfg, blob, offs, x_bits, budget_s, batch):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     out = {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads, "kind": "port",
-           "cpu": cpu_model(), "omp_threads": O.max_threads()}
+           "cpu": cpu_model(), "omp_threads": O.max_threads(), "host_cpus": host_cpus, "affinity_cpus": usable,
+           "threads_from": threads_from}
     sample = (f"{len(times)} frame(s) at batch 1 (8160 tokens x {cfg.n_blocks} blocks each), median "
               f"{med * 1e3:.1f} ms/frame")
     left = budget_s * 2 - (time.perf_counter() - t_start)
@@ -199,7 +207,9 @@ def cpu_baseline(cfg, blob, offs, x_bits, budget_s, batch):
         tb = time.perf_counter() - t0
         out["batch"] = {"frames": batch, "s": round(tb, 3), "frames_per_s": round(batch / tb, 4)}
         sample += f"; the batch of {batch} once, {tb:.2f} s"
-    out["sample"] = sample + f"; fp32 oracle (oracle/oracle.c) with OpenMP on {threads} threads, host CPU: {cpu_model()}"
+    out["sample"] = sample + (f"; fp32 oracle (oracle/oracle.c) with OpenMP on {threads} threads ({threads_from}) "
+                              f"of a host with {host_cpus} logical CPUs ({usable} in this process's affinity "
+                              f"mask), host CPU: {cpu_model()}")
     return out
 
 

@@ -72,7 +72,11 @@ typedef struct prism_block_offsets {
 /* Attention stage parameters: shaders/split2_qkv_attn_d256.comp.glsl:11-16
  * {n_tokens, dim, n_heads, head_dim, spatial_w, spatial_h, window_size,
  *  qkv_w, qkv_b, out_w, out_b, input_offset, output_offset} + LN1 offsets.
- * n_tokens is the per-frame token count and must equal spatial_w*spatial_h. */
+ * n_tokens is the per-frame token count and must equal spatial_w*spatial_h,
+ * and be at least 64: every window keys all 64 of its slots, which is the
+ * reference's key set (the first min(64, n_tokens) slots) exactly when a frame
+ * has 64 tokens or more; smaller frames are refused with
+ * PRISM_ERR_UNSUPPORTED (attention stage calls and the block chains). */
 typedef struct prism_attn_push {
     int32_t n_tokens, dim, n_heads, head_dim;
     int32_t spatial_w, spatial_h, window_size;

@@ -49,6 +49,12 @@ static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
  * the tokens. Smaller grids keep 64-token tiles (8 waves below 512 tiles). */
 static constexpr int EXPERT_WIDE_MIN_TILES = 512;
 
+/* Attention keys all 64 slots of a window. The reference keys the first
+ * min(64, n_tokens) slots in slot order (split2_qkv_attn_d256.comp.glsl:33,60),
+ * which differs only for frames of fewer than 64 tokens: those are refused. */
+static constexpr int ATTN_MIN_TOKENS = 64;
+#define ATTN_MIN_TOKENS_WHY "the reference keys only the first n_tokens window slots below 64 tokens"
+
 enum ChainMode { CHAIN_BLOCKS = 0, CHAIN_ADAPTED = 1, CHAIN_E2E = 2 };
 
 struct prism_ctx {

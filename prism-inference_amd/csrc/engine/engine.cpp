@@ -597,6 +597,9 @@ static int check_attn(prism_ctx* c, const prism_attn_push* p, void* features, in
     if (p->spatial_w < 1 || p->spatial_h < 1 || (int64_t)p->spatial_w * p->spatial_h != p->n_tokens)
         return fail(c, PRISM_ERR_INVALID, "n_tokens %d != spatial_w*spatial_h (%d*%d)", p->n_tokens, p->spatial_w,
                     p->spatial_h);
+    if (p->n_tokens < ATTN_MIN_TOKENS)
+        return fail(c, PRISM_ERR_UNSUPPORTED, "%d tokens per frame: attention needs at least %d (%s)", p->n_tokens,
+                    ATTN_MIN_TOKENS, ATTN_MIN_TOKENS_WHY);
     const DevBlock* k = find_block(c, p->qkv_w, 0);
     if (!k || k->offs.qkv_b != p->qkv_b || k->offs.out_w != p->out_w || k->offs.out_b != p->out_b ||
         k->offs.ln1_g != p->ln1_g || k->offs.ln1_b != p->ln1_b)
@@ -898,6 +901,9 @@ static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
     if (!in || !out) return fail(c, PRISM_ERR_INVALID, "in or out is NULL");
     if (!aligned16(in) || !aligned16(out)) return fail(c, PRISM_ERR_INVALID, "in/out must be 16-byte aligned");
     if (batch < 1) return fail(c, PRISM_ERR_INVALID, "batch %d < 1", batch);
+    if ((int64_t)c->desc.spatial_h * c->desc.spatial_w < ATTN_MIN_TOKENS)
+        return fail(c, PRISM_ERR_UNSUPPORTED, "%dx%d token grid: attention needs at least %d tokens per frame (%s)",
+                    c->desc.spatial_h, c->desc.spatial_w, ATTN_MIN_TOKENS, ATTN_MIN_TOKENS_WHY);
     return PRISM_OK;
 }
 
@@ -978,6 +984,9 @@ static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t ba
     if (rc) return rc;
     if (before) HIP_TRY(c, hipEventRecord(before, (hipStream_t)stream));
     HIP_TRY(c, hipGraphLaunch(c->gexec, (hipStream_t)stream));
+    /* the replayed chain writes its assignment rows at this token count (a
+     * capture sets it too, but a replay of a cached graph captures nothing) */
+    c->fwd_tokens = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
     return PRISM_OK;
 }
 

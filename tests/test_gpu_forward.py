@@ -75,15 +75,19 @@ EXTRA = {
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,H,W,batch", [
     ("moe64", 3, 68, 120, 1),      # 8-wave routed kernel, 4 router row tiles
-    ("moe64", 2, 68, 120, 4),      # 4-wave routed kernel (540 windows)
-    ("moe16", 2, 20, 28, 3),       # 1 row tile, ragged windows, 3 frames
+    ("moe64", 2, 68, 120, 4),      # two sub-chains of 2 frames (270 windows each): 8-wave kernels
+    ("moe16", 2, 20, 28, 3),       # 1 row tile, ragged windows, 3 frames (one chain)
     ("moe16", 1, 20, 28, 2),       # one block: its counters are cleared inside the chain
     ("moe40", 2, 68, 120, 1),
     ("moe40", 2, 68, 120, 4),
     ("moe24d128", 3, 68, 120, 1),
     ("moe24d128", 2, 68, 120, 4),
-    ("moe64", 2, 68, 120, 16),     # sub-chains of 8 frames: 128-token expert tiles
+    ("moe64", 2, 68, 120, 16),     # sub-chains of 8 frames: 4-wave _r4, 128-token expert tiles
     ("moe32", 2, 135, 240, 1),     # 510 windows, 8 waves, 2 router row tiles split over wave pairs
+    ("moe32", 2, 135, 240, 4),     # sub-chains of 2 frames (1020 windows each): 4-wave _r2
+    ("moe16", 2, 68, 120, 8),      # sub-chains of 4 frames (540 windows each): 4-wave _r1
+    ("moe40", 2, 68, 120, 8),      # 4-wave _r3
+    ("moe24d128", 2, 68, 120, 8),  # d128 4-wave _r2
 ])
 def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch):
     """The chain routes inside the attention kernel; the stage calls run the

@@ -49,7 +49,8 @@ def _reference(hip, device_arena, name, nb, H, W, batch, adapted, x):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,H,W,batch,adapted", [
-    ("moe16", 2, 20, 28, 3, False),   # two sub-chains (2 + 1 frames)
+    ("moe16", 2, 20, 28, 3, False),   # 3 frames: one chain (sub-chains start at 4 frames)
+    ("moe16", 2, 20, 28, 5, False),   # two sub-chains (2 + 3 frames)
     ("moe64", 2, 68, 120, 1, True),   # the adapted chain: 128-channel in/out
     ("dense128", 2, 68, 120, 4, False),
 ])

@@ -222,21 +222,43 @@ def test_experts_wide_tiles(hip, engine, device_arena, name, H, W, B):
 
 FUSED_EXTRA = {
     "moe40": P.Config("moe40", 256, 2, 8, 32, 40, 68, 120, 1, P.ROUTE_UNIFORM),
+    "moe32u": P.Config("moe32u", 256, 2, 8, 32, 32, 68, 120, 1, P.ROUTE_UNIFORM),
+    "moe16d128": P.Config("moe16d128", 128, 2, 8, 16, 16, 68, 120, 1, P.ROUTE_UNIFORM),
     "moe24d128": P.Config("moe24d128", 128, 2, 8, 16, 24, 68, 120, 1, P.ROUTE_ZIPF),
+    "moe40d128": P.Config("moe40d128", 128, 2, 8, 16, 40, 68, 120, 1, P.ROUTE_UNIFORM),
+    "moe64d128": P.Config("moe64d128", 128, 2, 8, 16, 64, 68, 120, 1, P.ROUTE_ZIPF),
 }
 
 
+def attn_kernel(dim, n_experts, windows):
+    """The attention kernel the engine launches for `windows` workgroups
+    (engine.cpp enqueue_attn): 8 waves below 512 windows, 4 waves from 512 on;
+    _r<k> routes over 16k padded experts."""
+    npt = (n_experts + 15) // 16 if n_experts > 1 else 0
+    return f"prism_attn_d{dim}{'_w8' if windows < 512 else ''}{f'_r{npt}' if npt else ''}"
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,H,W,batch", [
-    ("moe64", 68, 120, 1),      # 8-wave kernel
-    ("moe64", 68, 120, 4),      # 4-wave kernel
-    ("moe16", 9, 13, 1),        # one row tile, ragged windows
-    ("moe40", 68, 120, 1),      # 3 row tiles, 24 padded experts
-    ("moe24d128", 68, 120, 2),
+@pytest.mark.parametrize("name,H,W,batch,kernel", [
+    ("moe64", 68, 120, 1, "prism_attn_d256_w8_r4"),
+    ("moe64", 68, 120, 4, "prism_attn_d256_r4"),       # 540 windows
+    ("moe16", 9, 13, 1, "prism_attn_d256_w8_r1"),      # one row tile, ragged windows
+    ("moe40", 68, 120, 1, "prism_attn_d256_w8_r3"),    # 3 row tiles, 24 padded experts
+    ("moe24d128", 68, 120, 2, "prism_attn_d128_w8_r2"),
+    ("moe16", 68, 120, 4, "prism_attn_d256_r1"),
+    ("moe32u", 68, 120, 4, "prism_attn_d256_r2"),
+    ("moe40", 68, 120, 4, "prism_attn_d256_r3"),
+    ("moe16d128", 68, 120, 4, "prism_attn_d128_r1"),
+    ("moe24d128", 68, 120, 4, "prism_attn_d128_r2"),
+    ("moe40d128", 68, 120, 4, "prism_attn_d128_r3"),
+    ("moe64d128", 68, 120, 4, "prism_attn_d128_r4"),
 ])
-def test_attn_route_equals_attn_then_router(hip, engine, device_arena, name, H, W, batch):
-    """The fused launch leaves exactly what prism_attn + prism_router leave."""
+def test_attn_route_equals_attn_then_router(hip, engine, device_arena, name, H, W, batch, kernel):
+    """The fused launch leaves exactly what prism_attn + prism_router leave,
+    and its output and routing meet the oracle (every routed variant, 4 and 8
+    waves, d256 and d128)."""
     cfg = FUSED_EXTRA[name] if name in FUSED_EXTRA else P.CONFIGS[name]
+    assert attn_kernel(cfg.dim, cfg.n_experts, batch * ((H + 7) // 8) * ((W + 7) // 8)) == kernel
     desc, blob, offs, w = make_model(cfg, 2, H, W)
     engine.load_weights(desc, blob, offs)
     n, d, N = batch * H * W, cfg.dim, cfg.n_experts
@@ -267,6 +289,71 @@ def test_attn_route_equals_attn_then_router(hip, engine, device_arena, name, H, 
     perm_s, perm_f = auxs[n + N:].reshape(N, n), auxf[n + N:].reshape(N, n)
     for e in range(N):
         assert (np.sort(perm_s[e, :counts[e]]) == np.sort(perm_f[e, :counts[e]])).all(), f"bucket {e}"
+    # the fused kernel against the oracle
+    c = ocfg(cfg, H, W, batch)
+    h_ref = O.attn_stage(c, w, offs[1], f16(x))
+    mx, mean = errors(f16(hf).reshape(n, d), h_ref)
+    ref_assign, logits = O.router_stage(c, w, offs[1], h_ref)
+    top2 = np.sort(logits, axis=1)[:, -2:]
+    sure = (top2[:, 1] - top2[:, 0]) >= GAP
+    print(f"[attn_route] {name} ({kernel}): max {mx:.3g} mean {mean:.3g}, "
+          f"{int((auxf[:n] != ref_assign).sum())} of {n} experts differ, {int((~sure).sum())} near ties")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+    assert (auxf[:n][sure] == ref_assign[sure]).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 4])
+def test_non_finite_window_stays_in_its_window(hip, engine, device_arena, batch):
+    """Inf and NaN in one window's input rows (a defined result, not a fault):
+    that window's tokens come out non-finite and route to expert 0 (no
+    logit beats a NaN scan, as in moe_router.comp.glsl:40-45 where the strict
+    > never picks a NaN), the counts still sum to the token count, every
+    bucket entry names a token of its expert, and every other window's output
+    and routing are bit-identical to a clean run. The expert stage leaves
+    every token outside the window bit-identical as well."""
+    cfg = P.CONFIGS["moe64"]
+    H, W = 68, 120
+    desc, blob, offs, w = make_model(cfg, 1, H, W)
+    engine.load_weights(desc, blob, offs)
+    n, d, N, T = batch * H * W, cfg.dim, cfg.n_experts, H * W
+    x = P.synth_features(cfg, batch=batch, H=H, W=W, seed=4).reshape(n, d).copy()
+    # window (wy=2, wx=3) of the last frame: rows 16..23, columns 24..31
+    f = batch - 1
+    win = np.array([f * T + y * W + xx for y in range(16, 24) for xx in range(24, 32)])
+    bad = x.copy()
+    bad[win[0], 5] = 0x7C00        # +Inf
+    bad[win[9], 100] = 0xFC00      # -Inf
+    bad[win[20], :] = 0x7E00       # NaN row
+    aux_n = P.aux_elems(N, n)
+    runs = {}
+    for tag, xin in (("clean", x), ("poisoned", bad)):
+        feats = device_arena(3 * n * d * 2)
+        aux = device_arena(aux_n * 4)
+        hip.upload(feats.ptr, xin)
+        pa = engine.attn_push(0, 0, n * d, H, W)
+        pr = engine.router_push(0, T, n * d, 0, n, n + N)
+        print(f"[non-finite] batch {batch} {tag}", flush=True)
+        assert engine.attn_route(pa, pr, feats.ptr, aux.ptr, batch) == 0, engine.error()
+        push = engine.expert_push(0, T, n * d, 2 * n * d, 0, n, n + N)
+        assert engine.experts(push, feats.ptr, aux.ptr, batch) == 0, engine.error()
+        hip.sync()
+        h = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2).reshape(n, d)
+        y = hip.download(np.empty(n * d, np.uint16), feats.ptr + 2 * n * d * 2).reshape(n, d)
+        runs[tag] = (h, y, hip.download(np.empty(aux_n, np.int32), aux.ptr))
+    (h0, y0, a0), (h1, y1, a1) = runs["clean"], runs["poisoned"]
+    inside = np.zeros(n, bool)
+    inside[win] = True
+    assign, counts, perm = a1[:n], a1[n:n + N], a1[n + N:].reshape(N, n)
+    assert not np.isfinite(f16(h1[inside])).all(), "the poisoned window stayed finite"
+    assert (assign[inside] == 0).all(), "non-finite tokens must route to expert 0"
+    assert (h1[~inside] == h0[~inside]).all(), "a clean window changed"
+    assert (assign[~inside] == a0[:n][~inside]).all(), "a clean token's expert changed"
+    assert counts.sum() == n and (counts == np.bincount(assign, minlength=N)).all()
+    for e in range(N):
+        ids = perm[e, :counts[e]]
+        assert ((ids >= 0) & (ids < n)).all() and (np.sort(ids) == np.nonzero(assign == e)[0]).all(), f"bucket {e}"
+    assert (y1[~inside] == y0[~inside]).all(), "the expert stage changed a clean token"
 
 
 @pytest.mark.gpu
