@@ -220,6 +220,21 @@ int prism_forward(prism_ctx* ctx, const void* in, void* out, int32_t batch, void
 int prism_forward_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch,
                         void* stream);
 
+/* prism_forward without any allocation: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under hipGraph stream
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * launches as prism_forward, bit-identical output, but the chain's workspace
+ * (attention output, ping-pong rows, per-block assignments, routing
+ * counters, buckets) lives in a fixed per-GPU device array of 16 MiB that the
+ * library holds from prism_create until the process ends; the call itself
+ * allocates and frees nothing. A forward whose workspace exceeds 16 MiB
+ * (2*n*dim*2 + n_blocks*n*4 + n_experts*n*4 bytes + the counter rows, n =
+ * batch*H*W; e.g. MoE-64 d256 x 16 blocks at 68x120 fits at batch 1) is
+ * refused with PRISM_ERR_INVALID before any launch. The array keeps the last
+ * call's contents (the call clears the counters it needs first); calls on one
+ * GPU that overlap in time, from any context, share the array and race. */
+int prism_forward_noalloc(prism_ctx* ctx, const void* in, void* out, int32_t batch, void* stream);
+
 /* Device pointer to the expert assignment of every block of the most recent
  * forward: [n_blocks][batch*H*W] int32. */
 int prism_forward_assignments(prism_ctx* ctx, const int32_t** assign_dev,

@@ -55,6 +55,18 @@ static constexpr int EXPERT_WIDE_MIN_TILES = 512;
 static constexpr int ATTN_MIN_TOKENS = 64;
 #define ATTN_MIN_TOKENS_WHY "the reference keys only the first n_tokens window slots below 64 tokens"
 
+/* The block chain's working buffers for one forward: the engine's workspace
+ * or the allocation-free path's scratch. */
+struct ChainWs {
+    uint16_t* attn = nullptr;    /* [n][dim] attention output h            */
+    uint16_t* scratch = nullptr; /* [n][dim] ping-pong                     */
+    uint16_t* io = nullptr;      /* adapted chain: [n][dim] 256-channel rows */
+    int32_t* assign = nullptr;   /* [n_blocks][n]                          */
+    int32_t* counts = nullptr;   /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
+    int32_t* perm = nullptr;     /* per sub-chain j: [N][its tokens], back to back */
+    int64_t n = 0;               /* tokens of the forward (assignment row stride) */
+};
+
 enum ChainMode { CHAIN_BLOCKS = 0, CHAIN_ADAPTED = 1, CHAIN_E2E = 2 };
 
 struct prism_ctx {
@@ -85,14 +97,11 @@ struct prism_ctx {
     /* forward workspace */
     void* ws = nullptr;
     int ws_batch = 0;
-    uint16_t* ws_attn = nullptr;
-    uint16_t* ws_scratch = nullptr;
-    uint16_t* ws_io = nullptr;    /* adapted chain: 256-channel rows between blocks */
-    int32_t* ws_assign = nullptr; /* [n_blocks][n] */
-    int32_t* ws_counts = nullptr; /* [CHAIN_SPLIT][n_blocks][N][CHAIN_COUNT_STRIDE] */
-    int32_t* ws_perm = nullptr;   /* per half-chain j: [N][its tokens], back to back */
+    ChainWs wsb;                  /* its buffers (ws_batch frames)             */
     int64_t ws_tokens = 0;
     int64_t fwd_tokens = 0;       /* tokens per block of the last forward */
+    const int32_t* fwd_assign = nullptr; /* [n_blocks][fwd_tokens] of the last forward */
+    void* scratch = nullptr;      /* this device's allocation-free workspace (scratch.hip) */
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
     int32_t* stage_counts = nullptr; /* prism_attn_route: private counters, CHAIN_COUNT_STRIDE apart */
     bool stage_dirty = false;        /* ... possibly nonzero (a call stopped between its launches) */
@@ -123,6 +132,16 @@ struct prism_ctx {
     uint16_t *cbott = nullptr, *cchain = nullptr;             /* bottleneck in / chain out (e2e) */
     uint16_t *cd3 = nullptr, *cd2 = nullptr;
 };
+
+/* The allocation-free forward's workspace: one device array of this many
+ * bytes per GPU (scratch.hip), e.g. MoE-64 d256 x 16 blocks at 68x120 and
+ * batch 1 takes 11.5 MB of it. */
+static constexpr size_t PRISM_SCRATCH_BYTES = size_t(16) << 20;
+static constexpr int PRISM_SCRATCH_MAX_DEVICES = 64;
+
+/* scratch.hip: the scratch array's address on `device` (which must be the
+ * current device), taken once per device and kept. */
+hipError_t scratch_device_address(int device, void** out);
 
 /* Record the message on the context (if any) and the thread; returns code. */
 int fail(prism_ctx* c, int code, const char* fmt, ...);

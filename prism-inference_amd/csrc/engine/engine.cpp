@@ -83,6 +83,13 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         delete c;
         return fail(nullptr, PRISM_ERR_HIP, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
     }
+    /* this device's allocation-free workspace (prism_forward_noalloc) */
+    e = scratch_device_address(device, &c->scratch);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, PRISM_ERR_HIP, "device address of the scratch array on device %d: %s", device,
+                    hipGetErrorString(e));
+    }
     e = hipModuleLoad(&c->module, path.c_str());
     if (e != hipSuccess) {
         delete c;
@@ -166,8 +173,9 @@ static void drop_adapters(prism_ctx* c) {
 
 static void drop_workspace(prism_ctx* c) {
     if (c->ws) (void)hipFree(c->ws);
+    if (c->fwd_assign == c->wsb.assign) c->fwd_assign = nullptr;
     c->ws = nullptr;
-    c->ws_io = nullptr;
+    c->wsb = ChainWs{};
     c->ws_batch = 0;
     c->ws_tokens = 0;
 }
@@ -770,40 +778,59 @@ extern "C" int prism_project_down(prism_ctx* c, const prism_project_push* p, voi
 
 /* ------------------------------------------------------------ block chain */
 
-/* io: also the two chain-input/output buffers of the adapted chain */
+/* Byte offsets of the chain's buffers for n tokens (io: also the adapted
+ * chain's 256-channel buffer), from one base; returns the total size. */
+struct ChainLayout {
+    size_t attn, scr, asg, cnt, perm, io, bytes;
+};
+static ChainLayout chain_layout(const prism_model_desc& d, int64_t n, bool io) {
+    const size_t D = d.dim, N = d.n_experts, NB = d.n_blocks;
+    Arena ar;
+    ChainLayout L;
+    L.attn = ar.take((size_t)n * D * 2);
+    L.scr = ar.take((size_t)n * D * 2);
+    L.asg = ar.take(NB * (size_t)n * 4);
+    L.cnt = ar.take((size_t)CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE * 4);
+    L.perm = ar.take(N * (size_t)n * 4);
+    L.io = ar.take(io ? (size_t)n * D * 2 : 0);
+    L.bytes = ar.off;
+    return L;
+}
+
+static ChainWs chain_ws_at(void* base, const ChainLayout& L, int64_t n, bool io) {
+    uint8_t* b = static_cast<uint8_t*>(base);
+    ChainWs w;
+    w.attn = reinterpret_cast<uint16_t*>(b + L.attn);
+    w.scratch = reinterpret_cast<uint16_t*>(b + L.scr);
+    w.io = io ? reinterpret_cast<uint16_t*>(b + L.io) : nullptr;
+    w.assign = reinterpret_cast<int32_t*>(b + L.asg);
+    w.counts = reinterpret_cast<int32_t*>(b + L.cnt);
+    w.perm = reinterpret_cast<int32_t*>(b + L.perm);
+    w.n = n;
+    return w;
+}
+
+/* io: also the adapted chain's 256-channel buffer */
 static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
-    if (c->ws && c->ws_batch >= batch && (!io || c->ws_io)) return PRISM_OK;
-    io = io || (c->ws && c->ws_io); /* keep them once allocated */
+    if (c->ws && c->ws_batch >= batch && (!io || c->wsb.io)) return PRISM_OK;
+    io = io || (c->ws && c->wsb.io); /* keep it once allocated */
     drop_graph(c);
     drop_workspace(c);
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
-    const int D = c->desc.dim, N = c->desc.n_experts, NB = c->desc.n_blocks;
     if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
-    Arena ar;
-    const size_t o_attn = ar.take((size_t)n * D * 2);
-    const size_t o_scr = ar.take((size_t)n * D * 2);
-    const size_t o_asg = ar.take((size_t)NB * n * 4);
-    const size_t o_cnt = ar.take((size_t)CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE * 4);
-    const size_t o_perm = ar.take((size_t)N * n * 4);
-    const size_t o_io0 = ar.take(io ? (size_t)n * D * 2 : 0);
+    const ChainLayout L = chain_layout(c->desc, n, io);
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, ar.off);
-    if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for the workspace: %s", ar.off, hipGetErrorString(e));
-    e = hipMemset(p, 0, ar.off);
+    hipError_t e = hipMalloc(&p, L.bytes);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_NOMEM, "hipMalloc(%zu) for the workspace: %s", L.bytes, hipGetErrorString(e));
+    e = hipMemset(p, 0, L.bytes);
     if (e != hipSuccess) {
         (void)hipFree(p);
         return fail(c, PRISM_ERR_HIP, "hipMemset workspace: %s", hipGetErrorString(e));
     }
-    uint8_t* b = static_cast<uint8_t*>(p);
     c->ws = p;
     c->ws_batch = batch;
     c->ws_tokens = n;
-    c->ws_attn = reinterpret_cast<uint16_t*>(b + o_attn);
-    c->ws_scratch = reinterpret_cast<uint16_t*>(b + o_scr);
-    c->ws_assign = reinterpret_cast<int32_t*>(b + o_asg);
-    c->ws_counts = reinterpret_cast<int32_t*>(b + o_cnt);
-    c->ws_perm = reinterpret_cast<int32_t*>(b + o_perm);
-    c->ws_io = io ? reinterpret_cast<uint16_t*>(b + o_io0) : nullptr;
+    c->wsb = chain_ws_at(p, L, n, io);
     c->counts_dirty = false; /* zero-filled above */
     return PRISM_OK;
 }
@@ -823,19 +850,19 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
  * sub-chain's frames). adapted: in and out hold 128-channel rows; block 0's
  * attention runs the up-projection in its prologue and the last block's
  * expert stage the down-projection in its epilogue, the blocks in between
- * ping-pong through the 256-channel workspace (ws_io, ws_scratch). */
-static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t* in, uint16_t* out,
-                            hipStream_t s, bool adapted = false) {
+ * ping-pong through the 256-channel buffers (ws.io, ws.scratch). */
+static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int nf, const uint16_t* in,
+                            uint16_t* out, hipStream_t s, bool adapted = false) {
     const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w, D = c->desc.dim;
     const int N = c->desc.n_experts;
     const bool moe = N > 1;
-    const int64_t T = (int64_t)H * W, n = (int64_t)nf * T, t0 = (int64_t)f0 * T, n_all = c->fwd_tokens;
+    const int64_t T = (int64_t)H * W, n = (int64_t)nf * T, t0 = (int64_t)f0 * T, n_all = ws.n;
     const size_t row = (size_t)N * CHAIN_COUNT_STRIDE;
-    int32_t* counts0 = c->ws_counts + (size_t)j * NB * row;
-    int32_t* perm = c->ws_perm + (size_t)N * t0; /* this half's buckets: [N][n] */
-    uint16_t* attn = c->ws_attn + t0 * D;
-    uint16_t* scratch = c->ws_scratch + t0 * D;
-    uint16_t* mid = adapted ? c->ws_io + t0 * D : out; /* 256-channel stand-in for `out` */
+    int32_t* counts0 = ws.counts + (size_t)j * NB * row;
+    int32_t* perm = ws.perm + (size_t)N * t0; /* this half's buckets: [N][n] */
+    uint16_t* attn = ws.attn + t0 * D;
+    uint16_t* scratch = ws.scratch + t0 * D;
+    uint16_t* mid = adapted ? ws.io + t0 * D : out; /* 256-channel stand-in for `out` */
     if (moe && NB == 1) {
         const int rc = enqueue_zero(c, counts0, (int32_t)row, s);
         if (rc) return rc;
@@ -847,7 +874,7 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
         uint16_t* dst = last ? out : ((NB - 1 - b) % 2 == 0) ? mid : scratch;
         if (moe) {
             int32_t* counts = counts0 + (size_t)b * row;
-            const RouteOut ro{c->ws_assign + (size_t)b * n_all + t0, counts, perm, CHAIN_COUNT_STRIDE,
+            const RouteOut ro{ws.assign + (size_t)b * n_all + t0, counts, perm, CHAIN_COUNT_STRIDE,
                               NB > 1 ? counts0 + (size_t)((b + 1) % NB) * row : nullptr};
             int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro, first);
             if (rc) return rc;
@@ -864,13 +891,14 @@ static int enqueue_subchain(prism_ctx* c, int j, int f0, int nf, const uint16_t*
     return PRISM_OK;
 }
 
-static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, hipStream_t s,
-                                bool adapted = false) {
+static int enqueue_forward_impl(prism_ctx* c, const ChainWs& ws, const uint16_t* in, uint16_t* out, int batch,
+                                hipStream_t s, bool adapted = false) {
     const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w;
     const int64_t D = adapted ? c->aoffs.in_dim : c->desc.dim; /* channels of in and out */
     c->fwd_tokens = (int64_t)batch * T;
+    c->fwd_assign = ws.assign;
     const int S = std::max(1, std::min(CHAIN_SPLIT, batch / CHAIN_SPLIT_FRAMES));
-    if (S == 1) return enqueue_subchain(c, 0, 0, batch, in, out, s, adapted);
+    if (S == 1) return enqueue_subchain(c, ws, 0, 0, batch, in, out, s, adapted);
     /* fork: sub-chain j > 0 on sub_stream[j-1], sub-chain 0 on s, then join */
     HIP_TRY(c, hipEventRecord(c->ev_fork, s));
     int rc = PRISM_OK;
@@ -878,7 +906,7 @@ static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out,
         const int f0 = (int)((int64_t)batch * j / S), f1 = (int)((int64_t)batch * (j + 1) / S);
         hipStream_t sj = j ? c->sub_stream[j - 1] : s;
         if (j) HIP_TRY(c, hipStreamWaitEvent(sj, c->ev_fork, 0));
-        const int r = enqueue_subchain(c, j, f0, f1 - f0, in + f0 * T * D, out + f0 * T * D, sj, adapted);
+        const int r = enqueue_subchain(c, ws, j, f0, f1 - f0, in + f0 * T * D, out + f0 * T * D, sj, adapted);
         if (!rc) rc = r;
         if (j) HIP_TRY(c, hipEventRecord(c->ev_join[j - 1], sj));
     }
@@ -890,7 +918,7 @@ static int enqueue_forward_impl(prism_ctx* c, const uint16_t* in, uint16_t* out,
 static int clean_counts(prism_ctx* c, hipStream_t s) {
     if (!c->counts_dirty || c->desc.n_experts < 2) return PRISM_OK;
     /* every half-chain's counter rows (small) */
-    const int rc = enqueue_zero(c, c->ws_counts, CHAIN_SPLIT * c->desc.n_blocks * c->desc.n_experts * CHAIN_COUNT_STRIDE, s);
+    const int rc = enqueue_zero(c, c->wsb.counts, CHAIN_SPLIT * c->desc.n_blocks * c->desc.n_experts * CHAIN_COUNT_STRIDE, s);
     if (rc == PRISM_OK) c->counts_dirty = false;
     return rc;
 }
@@ -913,14 +941,16 @@ static int forward_checks(prism_ctx* c, const void* in, void* out, int batch) {
  * out); and that inside the encoder and decoder (CHAIN_E2E): encode(frame ->
  * cbott), adapted chain(cbott -> cchain), decode(cchain -> display). */
 static int enqueue_chain(prism_ctx* c, const uint16_t* in, uint16_t* out, int batch, int mode, hipStream_t s) {
-    if (mode == CHAIN_BLOCKS) return enqueue_forward_impl(c, in, out, batch, s);
+    ChainWs ws = c->wsb;
+    ws.n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w; /* rows of this forward */
+    if (mode == CHAIN_BLOCKS) return enqueue_forward_impl(c, ws, in, out, batch, s);
     if (mode == CHAIN_E2E) {
         int rc = codec_enqueue_encode(c, in, c->cbott, batch, s);
         if (!rc) rc = enqueue_chain(c, c->cbott, c->cchain, batch, CHAIN_ADAPTED, s);
         if (!rc) rc = codec_enqueue_decode(c, c->cchain, out, batch, s);
         return rc;
     }
-    return enqueue_forward_impl(c, in, out, batch, s, true);
+    return enqueue_forward_impl(c, ws, in, out, batch, s, true);
 }
 
 static int mode_ready(prism_ctx* c, int mode, int batch) {
@@ -987,6 +1017,7 @@ static int run_forward_graph(prism_ctx* c, const void* in, void* out, int32_t ba
     /* the replayed chain writes its assignment rows at this token count (a
      * capture sets it too, but a replay of a cached graph captures nothing) */
     c->fwd_tokens = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
+    c->fwd_assign = c->wsb.assign;
     return PRISM_OK;
 }
 
@@ -1014,10 +1045,38 @@ extern "C" int prism_forward_e2e_graph(prism_ctx* c, const void* frame, void* di
     return run_forward_graph(c, frame, display, batch, stream, CHAIN_E2E);
 }
 
+/* The eager chain with its workspace in this device's scratch array instead
+ * of the context's allocation: no hipMalloc / hipFree, ever. The counter rows
+ * are cleared by a fill launch first (the array keeps the previous call's
+ * contents); everything else is written before it is read. Calls that
+ * overlap on one GPU share the array and race. */
+extern "C" int prism_forward_noalloc(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
+    int rc = forward_checks(c, in, out, batch);
+    if (rc) return rc;
+    if (!c->scratch) return fail(c, PRISM_ERR_STATE, "no scratch array on device %d", c->device);
+    const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
+    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    const ChainLayout L = chain_layout(c->desc, n, false);
+    if (L.bytes > PRISM_SCRATCH_BYTES)
+        return fail(c, PRISM_ERR_INVALID,
+                    "prism_forward_noalloc: batch %d of %dx%d tokens needs %zu bytes of workspace, more than the "
+                    "%zu-byte scratch array (prism_forward allocates instead)",
+                    batch, c->desc.spatial_h, c->desc.spatial_w, L.bytes, (size_t)PRISM_SCRATCH_BYTES);
+    HIP_TRY(c, hipSetDevice(c->device));
+    const hipStream_t s = (hipStream_t)stream;
+    const ChainWs ws = chain_ws_at(c->scratch, L, n, false);
+    const int N = c->desc.n_experts, NB = c->desc.n_blocks;
+    if (N > 1) {
+        rc = enqueue_zero(c, ws.counts, CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE, s);
+        if (rc) return rc;
+    }
+    return enqueue_forward_impl(c, ws, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, s);
+}
+
 extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_dev, int64_t* tokens_per_block) {
     if (!c) return fail(nullptr, PRISM_ERR_INVALID, "context is NULL");
-    if (!c->ws) return fail(c, PRISM_ERR_STATE, "no forward has run");
-    if (assign_dev) *assign_dev = c->ws_assign;
+    if (!c->fwd_assign) return fail(c, PRISM_ERR_STATE, "no forward has run");
+    if (assign_dev) *assign_dev = c->fwd_assign;
     if (tokens_per_block) *tokens_per_block = c->fwd_tokens;
     return PRISM_OK;
 }

@@ -126,6 +126,7 @@ SIGNATURES = {
     "prism_experts": (C.c_int, [_P, C.POINTER(ExpertPush), _P, _P, C.c_int32, _P]),
     "prism_forward": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
     "prism_forward_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
+    "prism_forward_noalloc": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
     "prism_forward_assignments": (C.c_int, [_P, C.POINTER(_P), C.POINTER(C.c_int64)]),
     "prism_aux_elems": (C.c_int64, [C.c_int32, C.c_int64]),
     "prism_adapter_layout": (C.c_int, [C.POINTER(ModelDesc), C.c_int32, C.c_int64, C.POINTER(AdapterOffsets),
@@ -385,6 +386,7 @@ class Hip:
         L.hipGetErrorString.restype = C.c_char_p
         L.hipGetErrorString.argtypes = [C.c_int]
         L.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
+        L.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
 
     def _ok(self, rc, what):
         if rc != 0:
@@ -417,6 +419,12 @@ class Hip:
 
     def memset(self, p: int, value: int, nbytes: int):
         self._ok(self.L.hipMemset(C.c_void_p(p), value, nbytes), "hipMemset")
+
+    def mem_free(self) -> int:
+        """Free device memory in bytes (hipMemGetInfo)."""
+        free, total = C.c_size_t(), C.c_size_t()
+        self._ok(self.L.hipMemGetInfo(C.byref(free), C.byref(total)), "hipMemGetInfo")
+        return free.value
 
     def sync(self):
         self._ok(self.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
@@ -509,6 +517,11 @@ class Engine:
         else:
             f = self.L.prism_forward_graph if graph else self.L.prism_forward
         _check(f(self.h, x, y, batch, stream), self.h)
+
+    def forward_noalloc(self, x: int, y: int, batch: int, stream: int | None = None) -> int:
+        """prism_forward_noalloc: the eager chain on the device's scratch array
+        (no allocation); returns the status code."""
+        return self.L.prism_forward_noalloc(self.h, x, y, batch, stream)
 
     def infer_gpu(self, in_buf: int, in_offset: int, out_buf: int, out_offset: int, batch: int) -> float:
         """prism_infer_gpu: one synchronous inference between caller buffers; returns GPU ms."""
