@@ -358,27 +358,34 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                     s[kt] = mfma_16x16x16(k4[0][kt], q4[0][qt], f4_zero());
                 }
             }
-            float m = -3.0e38f;
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kt][i]);
-            m = max_groups(m);
+            const float m = max_groups(max16(s));
             /* exp(scale * (s - m)) = 2^(s * sl2 - m * sl2) */
             const float msl = m * sl2;
-            float sum = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 f4 e;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    e[i] = fast_exp2(__builtin_fmaf(s[kt][i], sl2, -msl));
-                    sum += e[i];
-                }
+                for (int i = 0; i < 4; ++i) e[i] = fast_exp2(__builtin_fmaf(s[kt][i], sl2, -msl));
                 p[kt][qt] = cvt_h4(e);
             }
-            sum = sum_groups(sum);
-            inv[qt] = fast_rcp(fmaxf(sum, 1e-6f));
+        }
+        /* The softmax denominators on the matrix cores: an all-ones A operand
+         * against P^T sums each query's 64 fp16 weights (the P that the P.V
+         * MFMAs use) into every lane of its column. */
+        {
+            const h8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt) {
+                f4 z = f4_zero();
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const h8 pb = {p[2 * st][qt][0], p[2 * st][qt][1], p[2 * st][qt][2], p[2 * st][qt][3],
+                                   p[2 * st + 1][qt][0], p[2 * st + 1][qt][1], p[2 * st + 1][qt][2],
+                                   p[2 * st + 1][qt][3]};
+                    z = mfma_16x16x32(ones, pb, z);
+                }
+                inv[qt] = fast_rcp(fmaxf(z[0], 1e-6f));
+            }
         }
 
         /* O^T[channel tile dt][query tile qt] = V^T P^T over 64 keys (2 k-steps) */

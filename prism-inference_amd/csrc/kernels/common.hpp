@@ -83,6 +83,16 @@ __device__ __forceinline__ float max_groups(float v) {
     return fmaxf(a, b);
 }
 
+/* Largest of the 16 values of four accumulators, as a tree of 3-input
+ * maxima (v_max3_f32). */
+__device__ __forceinline__ float max16(const f4 (&s)[4]) {
+    auto m3 = [](float a, float b, float c) { return fmaxf(fmaxf(a, b), c); };
+    const float a0 = m3(s[0][0], s[0][1], s[0][2]), a1 = m3(s[0][3], s[1][0], s[1][1]);
+    const float a2 = m3(s[1][2], s[1][3], s[2][0]), a3 = m3(s[2][1], s[2][2], s[2][3]);
+    const float a4 = m3(s[3][0], s[3][1], s[3][2]);
+    return fmaxf(m3(a0, a1, a2), m3(a3, a4, s[3][3]));
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
