@@ -169,7 +169,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
         for (int it = 0; it < IT; ++it) {
             const int s = wave * SPW + it * SPI + lane / LPS;
             const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-            rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM, valid[it]);
+            rc[it] = ln_load<DIM>(in + (int64_t)(valid[it] ? gy * a.W + gx : 0) * DIM); /* padded: row 0 */
         }
     } else {
 #pragma unroll

@@ -194,7 +194,7 @@ __device__ __forceinline__ h4 cvt_h4(f4 v) {
  * LayerNorm of rows into an LDS tile, LPS = DIM/16 lanes per row and 16
  * channels per lane, in two steps so a kernel can put every row load in
  * flight before it does any math: ln_load fetches the lane's 16 halfs of a
- * row (zeros for an invalid row), ln_store normalises them into `dst` (and
+ * row, ln_store normalises them into `dst` (and
  * copies the raw values to `raw_dst` if given). Lane i of a row holds
  * channels 8i..8i+7 and DIM/2+8i..+7, so each of the two 16-byte loads of a
  * wave reads contiguous half rows (whole cache lines, not every other 16
@@ -230,16 +230,14 @@ struct RowChunk {
     h8 a0, a1;
 };
 
+/* The caller passes an in-bounds row also for a padded or absent row (its
+ * values are then never used: ln_store writes zeros for it and its raw copy
+ * is never stored), so the load needs no zero fill and no branch. */
 template <int DIM>
-__device__ __forceinline__ RowChunk ln_load(const uint16_t* row, bool valid) {
+__device__ __forceinline__ RowChunk ln_load(const uint16_t* row) {
     constexpr int LPS = DIM / 16;
     const int ca = (lane_id() % LPS) * 8, cb = ca + DIM / 2;
-    RowChunk r{h8{}, h8{}};
-    if (valid) {
-        r.a0 = *reinterpret_cast<const h8*>(row + ca);
-        r.a1 = *reinterpret_cast<const h8*>(row + cb);
-    }
-    return r;
+    return RowChunk{*reinterpret_cast<const h8*>(row + ca), *reinterpret_cast<const h8*>(row + cb)};
 }
 
 template <int DIM>

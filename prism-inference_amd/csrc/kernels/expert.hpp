@@ -163,7 +163,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-            rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM, rt_tok[it] >= 0);
+            rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM); /* none: row 0 */
         }
         h8 wf[RT][KS];
 #pragma unroll
@@ -415,7 +415,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-        rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM, rt_tok[it] >= 0);
+        rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM); /* none: row 0 */
     }
     h8 ring[PF];
 #pragma unroll
@@ -470,7 +470,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
         const int tk = tok[wave * (BM / NW) + it * RPS + lane / CPR];
-        hx[it] = tk >= 0 ? *reinterpret_cast<const h8*>(a.in + (int64_t)tk * DIM + c8) : h8{};
+        hx[it] = *reinterpret_cast<const h8*>(a.in + (int64_t)(tk >= 0 ? tk : 0) * DIM + c8); /* none: row 0, unused */
     }
 #pragma unroll
     for (int r = 0; r < RT; ++r)
