@@ -169,7 +169,11 @@ const char* prism_last_error(const prism_ctx* ctx);
 
 /* Upload a weight blob (host memory, fp16, `bytes` long) laid out per offs
  * (desc->n_blocks entries) and repack it into the device's MFMA fragment
- * layout. Equivalent of PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611). */
+ * layout. Equivalent of PrismVulkan::LoadWeights (prism_vulkan.cpp:558-611).
+ * Each LayerNorm's gamma/beta is folded into the weights that consume its
+ * output (W' = r16(W diag(gamma)), b' = b + W beta); a folded weight that
+ * overflows fp16 fails with PRISM_ERR_BLOB, and the previous weights stay
+ * loaded. */
 int prism_load_weights(prism_ctx* ctx, const prism_model_desc* desc, const void* blob,
                        size_t bytes, const prism_block_offsets* offs);
 

@@ -17,9 +17,9 @@ struct DevBlock {
     prism_block_offsets offs;
     uint16_t* wqkv;
     float* bqkv;
+    float* bqkv_pad; /* the blob's QKV bias for padded window slots; NULL if LN1 beta = 0 */
     uint16_t* wo;
     float* bo;
-    float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
     uint16_t* wr;
     float* br;
     uint16_t* w1;

@@ -218,7 +218,7 @@ struct Arena {
 };
 
 struct BlockPlan {
-    size_t wqkv, bqkv, wo, bo, ln1_g, ln1_b, ln2_g, ln2_b, wr, br, w1, b1, w2, b2;
+    size_t wqkv, bqkv, bqkv_pad, wo, bo, wr, br, w1, b1, w2, b2;
 };
 
 inline int round16(int n) { return (n + 15) & ~15; }
@@ -243,12 +243,9 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
         BlockPlan& p = plan[b];
         p.wqkv = ar.take(3ull * D * D * 2);
         p.bqkv = ar.take(3ull * D * 4);
+        p.bqkv_pad = ar.take(3ull * D * 4);
         p.wo = ar.take(1ull * D * D * 2);
         p.bo = ar.take(D * 4);
-        p.ln1_g = ar.take(D * 4);
-        p.ln1_b = ar.take(D * 4);
-        p.ln2_g = ar.take(D * 4);
-        p.ln2_b = ar.take(D * 4);
         p.wr = ar.take((size_t)NP * D * 2);
         p.br = ar.take((size_t)NP * 4);
         p.w1 = ar.take((size_t)N * D * D * 2);
@@ -266,31 +263,41 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
         float* dst = reinterpret_cast<float*>(host.data() + at);
         for (int i = 0; i < n; ++i) dst[i] = half_to_float(s[i]);
     };
+    /* Each LayerNorm's affine goes into the weights that consume its output
+     * (LN1 -> W_qkv, LN2 -> W_r and every expert's W1): the kernels then only
+     * normalise, z = (x - mean) * inv, and W' = r16(W diag(gamma)),
+     * b' = b + W beta. With gamma = 1, beta = 0 the packed weights and biases
+     * are the blob's own values. */
+    std::vector<uint16_t> fw((size_t)3 * D * D);
+    auto fold_pack = [&](int64_t w, int rows, int rows_padded, int64_t gam, int64_t bet, int64_t bias, size_t dst_w,
+                         size_t dst_b, std::string* why) {
+        if (!fold_layernorm(src + w, rows, D, src + gam, src + bet, src + bias, fw.data(),
+                            reinterpret_cast<float*>(host.data() + dst_b), why))
+            return false;
+        pack_fragments(fw.data(), rows, D, rows_padded, reinterpret_cast<uint16_t*>(host.data() + dst_w));
+        return true;
+    };
     for (int b = 0; b < d->n_blocks; ++b) {
         const BlockPlan& p = plan[b];
         const prism_block_offsets& o = offs[b];
-        pack_fragments(src + o.qkv_w, 3 * D, D, 3 * D, reinterpret_cast<uint16_t*>(host.data() + p.wqkv));
-        f32(p.bqkv, src + o.qkv_b, 3 * D);
+        bool ok = fold_pack(o.qkv_w, 3 * D, 3 * D, o.ln1_g, o.ln1_b, o.qkv_b, p.wqkv, p.bqkv, &why);
+        f32(p.bqkv_pad, src + o.qkv_b, 3 * D); /* a padded slot's zero vector meets no beta */
         pack_fragments(src + o.out_w, D, D, D, reinterpret_cast<uint16_t*>(host.data() + p.wo));
         f32(p.bo, src + o.out_b, D);
-        f32(p.ln1_g, src + o.ln1_g, D);
-        f32(p.ln1_b, src + o.ln1_b, D);
-        f32(p.ln2_g, src + o.ln2_g, D);
-        f32(p.ln2_b, src + o.ln2_b, D);
-        if (N > 1) {
-            pack_fragments(src + o.router_w, N, D, NP, reinterpret_cast<uint16_t*>(host.data() + p.wr));
+        if (ok && N > 1) {
+            ok = fold_pack(o.router_w, N, NP, o.ln2_g, o.ln2_b, o.router_b, p.wr, p.br, &why);
             float* br = reinterpret_cast<float*>(host.data() + p.br);
-            for (int e = 0; e < NP; ++e) br[e] = e < N ? half_to_float(src[o.router_b + e]) : -INFINITY;
+            for (int e = N; e < NP; ++e) br[e] = -INFINITY;
         }
-        for (int e = 0; e < N; ++e) {
+        for (int e = 0; ok && e < N; ++e) {
             const int64_t eo = (int64_t)e * o.exp_stride;
-            pack_fragments(src + o.exp_w1 + eo, D, D, D,
-                           reinterpret_cast<uint16_t*>(host.data() + p.w1) + (size_t)e * D * D);
+            ok = fold_pack(o.exp_w1 + eo, D, D, o.ln2_g, o.ln2_b, o.exp_b1 + eo, p.w1 + (size_t)e * D * D * 2,
+                           p.b1 + (size_t)e * D * 4, &why);
             pack_fragments(src + o.exp_w2 + eo, D, D, D,
                            reinterpret_cast<uint16_t*>(host.data() + p.w2) + (size_t)e * D * D);
-            f32(p.b1 + (size_t)e * D * 4, src + o.exp_b1 + eo, D);
             f32(p.b2 + (size_t)e * D * 4, src + o.exp_b2 + eo, D);
         }
+        if (!ok) return fail(c, PRISM_ERR_BLOB, "block %d: %s", b, why.c_str());
     }
 
     (void)hipDeviceSynchronize();
@@ -317,12 +324,12 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
         k.offs = offs[b];
         k.wqkv = reinterpret_cast<uint16_t*>(base + p.wqkv);
         k.bqkv = reinterpret_cast<float*>(base + p.bqkv);
+        /* with LN1 beta = 0 the folded bias is the blob's: padded slots need nothing else */
+        bool beta1 = false;
+        for (int i = 0; i < D && !beta1; ++i) beta1 = (src[offs[b].ln1_b + i] & 0x7fff) != 0;
+        k.bqkv_pad = beta1 ? reinterpret_cast<float*>(base + p.bqkv_pad) : nullptr;
         k.wo = reinterpret_cast<uint16_t*>(base + p.wo);
         k.bo = reinterpret_cast<float*>(base + p.bo);
-        k.ln1_g = reinterpret_cast<float*>(base + p.ln1_g);
-        k.ln1_b = reinterpret_cast<float*>(base + p.ln1_b);
-        k.ln2_g = reinterpret_cast<float*>(base + p.ln2_g);
-        k.ln2_b = reinterpret_cast<float*>(base + p.ln2_b);
         k.wr = N > 1 ? reinterpret_cast<uint16_t*>(base + p.wr) : nullptr;
         k.br = N > 1 ? reinterpret_cast<float*>(base + p.br) : nullptr;
         k.w1 = reinterpret_cast<uint16_t*>(base + p.w1);
@@ -467,10 +474,9 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     a.out = out;
     a.wqkv = k.wqkv;
     a.bqkv = k.bqkv;
+    a.bqkv_pad = k.bqkv_pad;
     a.wo = k.wo;
     a.bo = k.bo;
-    a.ln_g = k.ln1_g;
-    a.ln_b = k.ln1_b;
     a.frame_elems = (int64_t)H * W * D;
     a.in_frame_elems = (int64_t)H * W * (up ? c->aoffs.in_dim : D);
     a.H = H;
@@ -481,8 +487,6 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     if (route) {
         const int N = c->desc.n_experts;
         npt = round16(N) / 16;
-        a.ln2_g = k.ln2_g;
-        a.ln2_b = k.ln2_b;
         a.wr = k.wr;
         a.br = k.br;
         a.assign = route->assign;
@@ -514,8 +518,6 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
     const int N = c->desc.n_experts;
     RouterArgs a{};
     a.in = in;
-    a.ln_g = k.ln2_g;
-    a.ln_b = k.ln2_b;
     a.wr = k.wr;
     a.br = k.br;
     a.assign = assign;
@@ -544,8 +546,6 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     }
     a.in = in;
     a.out = out;
-    a.ln_g = k.ln2_g;
-    a.ln_b = k.ln2_b;
     a.w1 = k.w1;
     a.b1 = k.b1;
     a.w2 = k.w2;

@@ -21,6 +21,12 @@ int validate_codec(const prism_model_desc* d, const prism_codec_offsets* c, int6
  * not the model's grid */
 bool codec_resolutions(const prism_model_desc* d, int render_w, int render_h, int* rw, int* rh, std::string* why);
 void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_t* dst);
+/* The LayerNorm affine moved into the weights that consume its output:
+ * Wf[o][i] = r16(W[o][i] * gamma[i]), bias_f[o] = bias[o] + sum_i W[o][i] * beta[i]
+ * (W row-major [rows][K], fp16; bias fp16). False (why) if a scaled weight
+ * overflows fp16. */
+bool fold_layernorm(const uint16_t* W, int rows, int K, const uint16_t* gamma, const uint16_t* beta,
+                    const uint16_t* bias, uint16_t* Wf, float* bias_f, std::string* why);
 float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);
 

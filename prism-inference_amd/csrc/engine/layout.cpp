@@ -9,8 +9,11 @@
  * reusing block 0's, and each tensor starts on an 8-element (16-byte)
  * boundary so the loader can use 16-byte loads.
  */
+#include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <string>
+#include <vector>
 
 #include "engine_internal.h"
 
@@ -172,6 +175,36 @@ void pack_fragments(const uint16_t* W, int rows, int K, int rows_padded, uint16_
                 else
                     memset(d, 0, 16);
             }
+}
+
+bool fold_layernorm(const uint16_t* W, int rows, int K, const uint16_t* gamma, const uint16_t* beta,
+                    const uint16_t* bias, uint16_t* Wf, float* bias_f, std::string* why) {
+    std::vector<float> g(K), be(K);
+    for (int i = 0; i < K; ++i) {
+        g[i] = half_to_float(gamma[i]);
+        be[i] = half_to_float(beta[i]);
+    }
+    for (int o = 0; o < rows; ++o) {
+        const uint16_t* wr = W + (size_t)o * K;
+        uint16_t* fr = Wf + (size_t)o * K;
+        double shift = 0.0;
+        for (int i = 0; i < K; ++i) {
+            const float w = half_to_float(wr[i]);
+            const float p = w * g[i]; /* exact: an fp16 x fp16 product fits fp32 */
+            const uint16_t h = float_to_half(p);
+            if ((h & 0x7c00) == 0x7c00 && std::isfinite(p)) {
+                if (why) *why = "LayerNorm gamma times weight overflows fp16 (row " + std::to_string(o) +
+                                ", channel " + std::to_string(i) + ")";
+                return false;
+            }
+            fr[i] = h;
+            shift += (double)w * (double)be[i];
+        }
+        const float b = half_to_float(bias[o]);
+        /* beta = 0 leaves the bias bit-identical (also a -0 bias) */
+        bias_f[o] = shift == 0.0 ? b : (float)((double)b + shift);
+    }
+    return true;
 }
 
 float half_to_float(uint16_t h) {

@@ -11,6 +11,11 @@
  *   W[16*rt + (l & 15)][32*ks + 8*(l >> 4) + j],  j = 0..7
  * at halfs ((rt*KS + ks)*64 + l)*8 + j, KS = K/32. One wave reads one
  * fragment with one fully coalesced 16-byte load per lane.
+ *
+ * LayerNorms carry no parameters here: the matrices that consume an LN's
+ * output (W_qkv for LN1; W_r and every expert's W1 for LN2) are stored with
+ * the LN affine folded in, W' = r16(W diag(gamma)) and b' = b + W beta, so a
+ * kernel only normalises, z = (x - mean) / sqrt(var + eps).
  */
 #ifndef PRISM_KERNEL_ARGS_H
 #define PRISM_KERNEL_ARGS_H
@@ -21,17 +26,17 @@ typedef struct AttnArgs {
     uint16_t* out;        /* features + output_offset                   */
     const uint16_t* wqkv; /* packed [3*dim/16][dim/32] fragments         */
     const float* bqkv;    /* [3*dim]                                     */
+    const float* bqkv_pad; /* [3*dim] the QKV of a padded window slot (whose
+                              LN1 output is the zero vector): the blob's bias,
+                              without LN1's beta term that bqkv carries;
+                              NULL when that term is zero (beta = 0)     */
     const uint16_t* wo;   /* packed [dim/16][dim/32]                     */
     const float* bo;      /* [dim]                                       */
-    const float* ln_g;    /* [dim]                                       */
-    const float* ln_b;    /* [dim]                                       */
     int64_t frame_elems;  /* H*W*dim                                     */
     int32_t H, W;         /* token grid                                  */
     int32_t wx;           /* windows per row = ceil(W/8)                 */
     int32_t windows_per_frame;
     /* fused routing (routed kernels only; the block chain's MoE blocks) */
-    const float* ln2_g;   /* [dim]                                       */
-    const float* ln2_b;   /* [dim]                                       */
     const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts 0 */
     const float* br;      /* [np]; entries >= n_experts are -inf          */
     int32_t* assign;      /* [cap] expert id per token                    */
@@ -57,8 +62,6 @@ typedef struct AttnArgs {
 
 typedef struct RouterArgs {
     const uint16_t* in;   /* features + input_offset                     */
-    const float* ln_g;
-    const float* ln_b;
     const uint16_t* wr;   /* packed [np/16][dim/32]; rows >= n_experts are 0 */
     const float* br;      /* [np]; entries >= n_experts are -inf          */
     int32_t* assign;      /* [n_tokens] expert id                         */
@@ -75,8 +78,6 @@ typedef struct RouterArgs {
 typedef struct ExpertArgs {
     const uint16_t* in;   /* h: features + input_offset                   */
     uint16_t* out;        /* features + output_offset                     */
-    const float* ln_g;
-    const float* ln_b;
     const uint16_t* w1;   /* packed, expert e at + e*dim*dim halfs        */
     const float* b1;      /* [n_experts][dim]                             */
     const uint16_t* w2;

@@ -7,7 +7,10 @@
  *
  *  1. LN1 of the window's 64 slots -> xs (LDS, fp16), the raw rows -> os
  *     (they are the residual; the out-proj's epilogue reads them from there,
- *     so x is fetched from HBM once). Padded slots are zero. With a fused
+ *     so x is fetched from HBM once). Padded slots are zero, so their keys
+ *     and values are the bias (with LN1's affine folded into W_qkv and the
+ *     bias, a block with beta != 0 gives padded windows the PAD body, which
+ *     restores the blob's own bias there). With a fused
  *     up-projection (the adapted chain's first block) the input rows have 128
  *     channels and x = r16(ReLU(W_up e + b_up)) is computed into os first
  *     (shaders/pw_project_128to256.comp.glsl:25-37, as project.hpp).
@@ -38,7 +41,8 @@
  * register ring PF fragments deep, so loads run 2 k-steps ahead of the MFMAs
  * and the next head's and the out-proj's first fragments are in flight while
  * the softmax math runs. All workgroups read the same 0.5 MiB per block,
- * which stays L2-resident. Biases and LN parameters are staged in LDS once.
+ * which stays L2-resident. Biases are staged in LDS once; the LayerNorms'
+ * affines are folded into W_qkv and W_r on the host.
  */
 #pragma once
 #include "route.hpp"
@@ -89,28 +93,45 @@ __device__ __forceinline__ h8 attn_frag(const FragSrc& wqkv, const FragSrc& wo, 
     return wr.load((rt0 + q % R) * S::KS + q / R, loff);
 }
 
-template <int DIM, int HD, int NW, int NPT>
-__device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
+/* The workgroup's LDS, declared once per kernel: both instantiations of the
+ * body (windows with and without padded slots) use the same arrays. */
+template <int DIM, int NPT>
+struct AttnLds {
+    __attribute__((aligned(16))) f16 xs[64 * (DIM + 8)];
+    __attribute__((aligned(16))) f16 os[64 * (DIM + 8)];
+    float bqkv[3 * DIM];
+    float bqkv_pad[3 * DIM]; /* PAD bodies only */
+    float bo[DIM];
+    float br[NPT > 0 ? 16 * NPT : 1]; /* router bias */
+};
+
+/* PAD: the window has padded slots and the block's LN1 beta is not zero, so
+ * those slots' keys and values need the unfolded bias (a separate
+ * instantiation keeps that code, and its branches, out of every other
+ * window's instruction schedule). vmask bit s: slot s holds a token. */
+template <int DIM, int HD, int NW, int NPT, bool PAD>
+__device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM, NPT>& L,
+                                                 unsigned long long vmask) {
     static_assert(DIM / HD == 8, "8 heads");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(NPT >= 0 && NPT <= 4, "up to 64 experts");
     using S = AttnShape<DIM, HD, NW, NPT>;
     constexpr int NT = 64 * NW;         /* threads                         */
-    constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT, PF = S::PF;
+    constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT;
+    /* ring depth: 2 k-steps ahead; 1 in the rare PAD body, whose padded-slot
+     * fix-up needs the registers */
+    constexpr int PF = PAD ? S::FPK : S::PF;
     constexpr float LOG2E = 1.4426950408889634f;
     const float scale = (HD == 32) ? 0.1767766953f : 1.0f / sqrtf((float)HD);
     const float sl2 = scale * LOG2E;
 
-    __shared__ __attribute__((aligned(16))) f16 xs[64 * LDS];
-    __shared__ __attribute__((aligned(16))) f16 os[64 * LDS];
-    __shared__ float s_bqkv[3 * DIM];
-    __shared__ float s_bo[DIM];
-    __shared__ float s_g[DIM];          /* LN1 */
-    __shared__ float s_b[DIM];
-    constexpr int RDIM = NPT > 0 ? DIM : 1;
-    __shared__ float s_g2[RDIM];        /* LN2 (routing) */
-    __shared__ float s_b2[RDIM];
-    __shared__ float s_br[NPT > 0 ? 16 * NPT : 1]; /* router bias */
+    static_assert(LDS == DIM + 8, "LDS row");
+    f16* const xs = L.xs;
+    f16* const os = L.os;
+    float* const s_bqkv = L.bqkv;
+    float* const s_bqkv_pad = L.bqkv_pad;
+    float* const s_bo = L.bo;
+    float* const s_br = L.br;
     /* routing scratch aliases the QKV biases, dead after the barrier ahead of
      * the out-proj */
     static_assert(3 * DIM >= 5 * 64, "routing scratch fits the QKV bias area");
@@ -200,15 +221,9 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     /* every parameter is staged now: a load issued after the residual
      * prefetch below would make its LDS store wait for that HBM fetch */
     for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
-    for (int i = threadIdx.x; i < DIM; i += NT) {
-        s_bo[i] = a.bo[i];
-        s_g[i] = a.ln_g[i];
-        s_b[i] = a.ln_b[i];
-        if constexpr (NPT > 0) {
-            s_g2[i] = a.ln2_g[i];
-            s_b2[i] = a.ln2_b[i];
-        }
-    }
+    if constexpr (PAD)
+        for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv_pad[i] = a.bqkv_pad[i];
+    for (int i = threadIdx.x; i < DIM; i += NT) s_bo[i] = a.bo[i];
     if constexpr (NPT > 0)
         for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
     __syncthreads(); /* parameters staged */
@@ -216,7 +231,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
-            ln_store<DIM>(rc[it], valid[it], s_g, s_b, xs + row, os + row); /* os: the raw rows (residual) */
+            ln_store<DIM>(rc[it], valid[it], xs + row, os + row); /* os: the raw rows (residual) */
         }
     } else {
         /* x = r16(ReLU(W_up e + b_up)) for the window's slots, the same
@@ -266,7 +281,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             const int ca = (lane % LPS) * 8;
             const RowChunk xr{*reinterpret_cast<const h8*>(os + row + ca),
                               *reinterpret_cast<const h8*>(os + row + ca + DIM / 2)};
-            ln_store<DIM>(xr, valid[it], s_g, s_b, xs + row, nullptr);
+            ln_store<DIM>(xr, valid[it], xs + row, nullptr);
         }
     }
     __syncthreads();
@@ -338,6 +353,35 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                 v4[t][c] = cvt_h4(accV[t][c]);
             }
 
+        /* A padded slot's input is the zero vector, so its key and value are
+         * r16 of the bias alone, without the LN1 beta term (W beta) that
+         * bqkv carries for the window's tokens. (Its query and output are
+         * never used.) */
+        if constexpr (PAD) {
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+                const int chk = DIM + h * HD + 16 * c + 4 * g;
+                const h4 bk = cvt_h4(f4{s_bqkv_pad[chk], s_bqkv_pad[chk + 1], s_bqkv_pad[chk + 2],
+                                        s_bqkv_pad[chk + 3]});
+                const f16 bv = (f16)s_bqkv_pad[2 * DIM + h * HD + 16 * c + l16];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    /* slots 16t..16t+15 (uniform): all present, all padded
+                     * (a bottom-edge window's last rows), or mixed */
+                    const unsigned tm = (unsigned)(vmask >> (16 * t)) & 0xffffu;
+                    if (tm == 0u) {
+                        k4[c][t] = bk;
+                        v4[t][c] = h4{bv, bv, bv, bv};
+                    } else if (tm != 0xffffu) {
+                        if (!((tm >> l16) & 1u)) k4[c][t] = bk;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (!((tm >> (4 * g + i)) & 1u)) v4[t][c][i] = bv;
+                    }
+                }
+            }
+        }
+
         /* Per query tile qt: S^T[kt] (element i = key 16kt+4g+i, query 16qt+l16),
          * softmax down the key axis (16 values in-lane, then the 4 lane groups),
          * P kept as fp16 operands for the P.V MFMA. */
@@ -384,7 +428,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
                                    p[2 * st + 1][qt][3]};
                     z = mfma_16x16x32(ones, pb, z);
                 }
-                inv[qt] = fast_rcp(fmaxf(z[0], 1e-6f));
+                inv[qt] = fast_rcp(vmax(z[0], 1e-6f));
             }
         }
 
@@ -491,7 +535,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
             float bv;
             int be;
-            route_partial<DIM, S::RPT>(cur, s_g2, s_b2, s_br, g, wave >= 4 ? S::RPT : 0, rfrag, bv, be);
+            route_partial<DIM, S::RPT>(cur, s_br, g, wave >= 4 ? S::RPT : 0, rfrag, bv, be);
             if (wave >= 4 && g == 0) {
                 r_pv[sl] = bv;
                 r_pe[sl] = be;
@@ -514,7 +558,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
             h8 cur[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
-            const int e = route_token<DIM, NPT>(cur, s_g2, s_b2, s_br, g, a.n_experts, rfrag);
+            const int e = route_token<DIM, NPT>(cur, s_br, g, a.n_experts, rfrag);
             if (g == 0) {
                 r_e[sl] = e;
                 r_rank[sl] = (sy < a.H && sx < a.W) ? atomicAdd(&r_hist[e], 1) : 0;
@@ -556,15 +600,29 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a) {
     }
 }
 
+template <int DIM, int HD, int NW, int NPT>
+__device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>& L) {
+    const int wi = blockIdx.x % a.windows_per_frame;
+    const int wy = wi / a.wx, wxx = wi - (wi / a.wx) * a.wx;
+    const int lane = lane_id();
+    const unsigned long long vmask = __ballot(wy * 8 + (lane >> 3) < a.H && wxx * 8 + (lane & 7) < a.W);
+    if (a.bqkv_pad != nullptr && vmask != ~0ull) /* uniform */
+        attn_window_body<DIM, HD, NW, NPT, true>(a, L, vmask);
+    else
+        attn_window_body<DIM, HD, NW, NPT, false>(a, L, vmask);
+}
+
 /* 4 waves (2 heads each, 2 workgroups per CU) for large grids; 8 waves (one
  * head each, one workgroup per CU) when windows are scarcer than CUs. The
  * _r<NPT> kernels also route the window's tokens (16*NPT padded experts). */
 #define PRISM_ATTN_KERNELS(D, HD, NPT, SUF)                                                          \
     extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d##D##SUF(AttnArgs a) {          \
-        attn_window_body<D, HD, 4, NPT>(a);                                                          \
+        __shared__ AttnLds<D, NPT> lds;                                                              \
+        attn_window<D, HD, 4, NPT>(a, lds);                                                          \
     }                                                                                                \
     extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d##D##_w8##SUF(AttnArgs a) {     \
-        attn_window_body<D, HD, 8, NPT>(a);                                                          \
+        __shared__ AttnLds<D, NPT> lds;                                                              \
+        attn_window<D, HD, 8, NPT>(a, lds);                                                          \
     }
 PRISM_ATTN_KERNELS(256, 32, 0, )
 PRISM_ATTN_KERNELS(256, 32, 1, _r1)

@@ -76,21 +76,27 @@ __device__ __forceinline__ float sum_groups(float v) {
     lanes_x32(a + b, a, b);
     return a + b;
 }
+/* NaN-propagating maximum (IEEE 754-2019 maximum, v_maximum3_f32 on gfx950).
+ * Unlike fmaxf it needs no canonicalising copy of operands the compiler
+ * cannot prove canonical (MFMA results, cross-lane moves): one instruction
+ * per 2 or 3 inputs. A NaN among the inputs gives NaN. */
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
+
 __device__ __forceinline__ float max_groups(float v) {
     float a, b;
     lanes_x16(v, a, b);
-    lanes_x32(fmaxf(a, b), a, b);
-    return fmaxf(a, b);
+    lanes_x32(vmax(a, b), a, b);
+    return vmax(a, b);
 }
 
 /* Largest of the 16 values of four accumulators, as a tree of 3-input
- * maxima (v_max3_f32). */
+ * maxima (NaN if any is NaN). */
 __device__ __forceinline__ float max16(const f4 (&s)[4]) {
-    auto m3 = [](float a, float b, float c) { return fmaxf(fmaxf(a, b), c); };
-    const float a0 = m3(s[0][0], s[0][1], s[0][2]), a1 = m3(s[0][3], s[1][0], s[1][1]);
-    const float a2 = m3(s[1][2], s[1][3], s[2][0]), a3 = m3(s[2][1], s[2][2], s[2][3]);
-    const float a4 = m3(s[3][0], s[3][1], s[3][2]);
-    return fmaxf(m3(a0, a1, a2), m3(a3, a4, s[3][3]));
+    const float a0 = vmax3(s[0][0], s[0][1], s[0][2]), a1 = vmax3(s[0][3], s[1][0], s[1][1]);
+    const float a2 = vmax3(s[1][2], s[1][3], s[2][0]), a3 = vmax3(s[2][1], s[2][2], s[2][3]);
+    const float a4 = vmax3(s[3][0], s[3][1], s[3][2]);
+    return vmax(vmax3(a0, a1, a2), vmax3(a3, a4, s[3][3]));
 }
 
 template <int CTRL>
@@ -198,15 +204,17 @@ __device__ __forceinline__ h4 cvt_h4(f4 v) {
  * copies the raw values to `raw_dst` if given). Lane i of a row holds
  * channels 8i..8i+7 and DIM/2+8i..+7, so each of the two 16-byte loads of a
  * wave reads contiguous half rows (whole cache lines, not every other 16
- * bytes of them). Two-pass mean / biased variance in fp32; output rounded to
- * fp16; invalid rows are written as zeros. g and b live in LDS.
+ * bytes of them). Mean / biased variance in fp32; output rounded to fp16;
+ * invalid rows are written as zeros. The affine is folded into the next
+ * GEMM's weights on the host, so there are no gamma/beta here.
  */
 /* LayerNorm building blocks (biased variance, eps 1e-5, fp32 statistics):
  * the sum and the sum of squares of fp16 values come straight from the fp16
  * pairs on v_dot2_f32_f16 (products exact, fp32 accumulation), the variance
  * is E[x^2] - mean^2 (clamped at 0), and each value is normalised as
- * z = fma(x, inv, -mean*inv) with the fp16 x as a mixed-precision operand,
- * then y = fma(z, gamma, beta). */
+ * z = fma(x, inv, -mean*inv) with the fp16 x as a mixed-precision operand
+ * (one instruction per value; gamma and beta live in the consuming GEMM's
+ * weights and bias). */
 __device__ __forceinline__ void moments8(const h8& x, float& s, float& q) {
     const h2 one = {(f16)1.0f, (f16)1.0f};
 #pragma unroll
@@ -222,8 +230,8 @@ __device__ __forceinline__ float ln_inv(float s, float q, float& mean) {
     const float var = fmaxf(__builtin_fmaf(-mean, mean, q * (1.0f / N)), 0.f);
     return __builtin_amdgcn_rsqf(var + PRISM_LN_EPS); /* v_rsq_f32, 1 ulp; argument >= 1e-5 */
 }
-__device__ __forceinline__ float ln_apply(f16 x, float inv, float nmi, float g, float b) {
-    return __builtin_fmaf(__builtin_fmaf((float)x, inv, nmi), g, b);
+__device__ __forceinline__ float ln_apply(f16 x, float inv, float nmi) {
+    return __builtin_fmaf((float)x, inv, nmi);
 }
 
 struct RowChunk {
@@ -240,9 +248,10 @@ __device__ __forceinline__ RowChunk ln_load(const uint16_t* row) {
     return RowChunk{*reinterpret_cast<const h8*>(row + ca), *reinterpret_cast<const h8*>(row + cb)};
 }
 
-template <int DIM>
-__device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const float* g, const float* b,
-                                         f16* dst, f16* raw_dst) {
+/* ZERO = false: the caller never uses an invalid row's output (its GEMM
+ * column is never stored), so it is left as computed from the stand-in row. */
+template <int DIM, bool ZERO = true>
+__device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, f16* dst, f16* raw_dst) {
     constexpr int LPS = DIM / 16;
     const int ca = (lane_id() % LPS) * 8, cb = ca + DIM / 2;
     if (raw_dst) {
@@ -260,14 +269,10 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const f
     h8 o0, o1;
 #pragma unroll
     for (int j = 0; j < 8; j += 4) {
-        const f4 n0 = {ln_apply(rc.a0[j], inv, nmi, g[ca + j], b[ca + j]),
-                       ln_apply(rc.a0[j + 1], inv, nmi, g[ca + j + 1], b[ca + j + 1]),
-                       ln_apply(rc.a0[j + 2], inv, nmi, g[ca + j + 2], b[ca + j + 2]),
-                       ln_apply(rc.a0[j + 3], inv, nmi, g[ca + j + 3], b[ca + j + 3])};
-        const f4 n1 = {ln_apply(rc.a1[j], inv, nmi, g[cb + j], b[cb + j]),
-                       ln_apply(rc.a1[j + 1], inv, nmi, g[cb + j + 1], b[cb + j + 1]),
-                       ln_apply(rc.a1[j + 2], inv, nmi, g[cb + j + 2], b[cb + j + 2]),
-                       ln_apply(rc.a1[j + 3], inv, nmi, g[cb + j + 3], b[cb + j + 3])};
+        const f4 n0 = {ln_apply(rc.a0[j], inv, nmi), ln_apply(rc.a0[j + 1], inv, nmi),
+                       ln_apply(rc.a0[j + 2], inv, nmi), ln_apply(rc.a0[j + 3], inv, nmi)};
+        const f4 n1 = {ln_apply(rc.a1[j], inv, nmi), ln_apply(rc.a1[j + 1], inv, nmi),
+                       ln_apply(rc.a1[j + 2], inv, nmi), ln_apply(rc.a1[j + 3], inv, nmi)};
         const h4 p0 = cvt_h4(n0), p1 = cvt_h4(n1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -275,10 +280,10 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, const f
             o1[j + i] = p1[i];
         }
     }
-    /* padded / missing rows are zero: select on whole 32-bit words */
+    /* with ZERO, padded / missing rows are zero: select on whole 32-bit words */
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
     u4 w0 = __builtin_bit_cast(u4, o0), w1 = __builtin_bit_cast(u4, o1);
-    const unsigned int keep = valid ? 0xffffffffu : 0u;
+    const unsigned int keep = (valid || !ZERO) ? 0xffffffffu : 0u;
     w0 &= keep;
     w1 &= keep;
     *reinterpret_cast<h8*>(dst + ca) = __builtin_bit_cast(h8, w0);

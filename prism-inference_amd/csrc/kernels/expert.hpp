@@ -63,11 +63,11 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
 }
 
 /* Tile scheduler (see the file comment): wave 0 finds this workgroup's
- * (expert, first row, row count), or expert -1 past the last tile; the other
- * waves stage the LayerNorm parameters meanwhile. The caller synchronises. */
+ * (expert, first row, row count), or expert -1 past the last tile. The
+ * caller synchronises. */
 template <int DIM, int BM, int NT>
-__device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, int lane, float* s_g, float* s_b,
-                                                int& sh_e, int& sh_row0, int& sh_rows) {
+__device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, int lane, int& sh_e, int& sh_row0,
+                                                int& sh_rows) {
     const int per_xcd = gridDim.x / 8;
     const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (wave == 0) {
@@ -89,11 +89,6 @@ __device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, i
             sh_e = row0 < a.n_tokens ? 0 : -1;
             sh_row0 = row0;
             sh_rows = min(BM, a.n_tokens - row0);
-        }
-    } else {
-        for (int i = threadIdx.x - 64; i < DIM; i += NT - 64) {
-            s_g[i] = a.ln_g[i];
-            s_b[i] = a.ln_b[i];
         }
     }
 }
@@ -131,7 +126,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 
     __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, then GELU output */
     __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
-    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
+    __shared__ float s_b1[DIM], s_b2[DIM];
     __shared__ int tok[BM];
     __shared__ int sh_e, sh_row0, sh_rows;
 
@@ -141,7 +136,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     const int g = lane >> 4;
 
     /* ---- schedule ------------------------------------------------------ */
-    expert_schedule<DIM, BM, NT>(a, wave, lane, s_g, s_b, sh_e, sh_row0, sh_rows);
+    expert_schedule<DIM, BM, NT>(a, wave, lane, sh_e, sh_row0, sh_rows);
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_e);
 
@@ -174,7 +169,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int r = wave * (BM / NW) + it * RPI + lane / LPS;
-            ln_store<DIM>(rc[it], rt_tok[it] >= 0, s_g, s_b, xs + r * LDS, hs + r * LDS);
+            ln_store<DIM, false>(rc[it], rt_tok[it] >= 0, xs + r * LDS, hs + r * LDS);
         }
         __syncthreads();
 
@@ -384,7 +379,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
     static_assert(RT >= 1 && BM % (NW * RPI) == 0 && PF % RT == 0 && PF <= NF, "tile shape");
 
     __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, GELU output, y */
-    __shared__ float s_b1[DIM], s_b2[DIM], s_g[DIM], s_b[DIM];
+    __shared__ float s_b1[DIM], s_b2[DIM];
     __shared__ int tok[BM];
     __shared__ int sh_e, sh_row0, sh_rows;
 
@@ -393,7 +388,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
     const int l16 = lane & 15;
     const int g = lane >> 4;
 
-    expert_schedule<DIM, BM, NT>(a, wave, lane, s_g, s_b, sh_e, sh_row0, sh_rows);
+    expert_schedule<DIM, BM, NT>(a, wave, lane, sh_e, sh_row0, sh_rows);
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_e);
     if (e < 0) return;
@@ -424,7 +419,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int r = wave * (BM / NW) + it * RPI + lane / LPS;
-        ln_store<DIM>(rc[it], rt_tok[it] >= 0, s_g, s_b, xs + r * LDS, nullptr);
+        ln_store<DIM, false>(rc[it], rt_tok[it] >= 0, xs + r * LDS, nullptr);
     }
     __syncthreads();
 

@@ -3,7 +3,8 @@
  * attention kernel's fused routing epilogue.
  *
  * Restates shaders/moe_router.comp.glsl:24-52 widened to N logits
- * (moe_ffn_16exp.comp.glsl:27-34): hn = LN2(h), logits = r16(W_r hn + b_r),
+ * (moe_ffn_16exp.comp.glsl:27-34): hn = LN2(h), logits = r16(W_r hn + b_r)
+ * (LN2's affine folded into W_r and b_r on the host),
  * expert = first index of the maximum (strict >, moe_router.comp.glsl:42-45).
  *
  * Lane layout (one 16-token tile per wave): lane (g = lane >> 4, l16 = lane & 15)
@@ -18,11 +19,10 @@
 #pragma once
 #include "common.hpp"
 
-/* hn = r16(LN2(h)) in the same lane layout as cur (the B operand of the
- * router GEMM). */
+/* hn = r16((h - mean) / sqrt(var + eps)) in the same lane layout as cur (the
+ * B operand of the router GEMM). */
 template <int DIM>
-__device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b, int g,
-                                         h8 (&hn)[DIM / 32]) {
+__device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], h8 (&hn)[DIM / 32]) {
     constexpr int KS = DIM / 32;
     float s = 0.f, q = 0.f;
 #pragma unroll
@@ -34,15 +34,11 @@ __device__ __forceinline__ void route_ln(const h8 (&cur)[DIM / 32], const float*
     const float nmi = -mean * inv;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        asm volatile("" ::: "memory"); /* keep this k-step's gamma/beta reads here */
 #pragma unroll
         for (int j = 0; j < 8; j += 4) {
             f4 t;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = 32 * ks + 8 * g + j + i;
-                t[i] = ln_apply(cur[ks][j + i], inv, nmi, s_g[c], s_b[c]);
-            }
+            for (int i = 0; i < 4; ++i) t[i] = ln_apply(cur[ks][j + i], inv, nmi);
             const h4 q4 = cvt_h4(t);
 #pragma unroll
             for (int i = 0; i < 4; ++i) hn[ks][j + i] = q4[i];
@@ -89,12 +85,11 @@ __device__ __forceinline__ void route_combine_groups(float& best_v, int& best_e)
  * lower id, so the best of consecutive ranges merged in range order with
  * route_pick equals the best of their union. */
 template <int DIM, int NR, class Frag>
-__device__ __forceinline__ void route_partial(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
-                                              const float* s_br, int g, int rt0, Frag&& frag, float& best_v,
-                                              int& best_e) {
+__device__ __forceinline__ void route_partial(const h8 (&cur)[DIM / 32], const float* s_br, int g, int rt0,
+                                              Frag&& frag, float& best_v, int& best_e) {
     constexpr int KS = DIM / 32;
     h8 hn[KS];
-    route_ln<DIM>(cur, s_g, s_b, g, hn);
+    route_ln<DIM>(cur, hn);
     f4 acc[NR]; /* starts at the router bias */
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -115,11 +110,11 @@ __device__ __forceinline__ void route_partial(const h8 (&cur)[DIM / 32], const f
 /* The token's expert over all NPT row tiles (frag(rt, ks) as above with
  * rt0 = 0), in all 4 lane groups of its column. */
 template <int DIM, int NPT, class Frag>
-__device__ __forceinline__ int route_token(const h8 (&cur)[DIM / 32], const float* s_g, const float* s_b,
-                                           const float* s_br, int g, int n_experts, Frag&& frag) {
+__device__ __forceinline__ int route_token(const h8 (&cur)[DIM / 32], const float* s_br, int g, int n_experts,
+                                           Frag&& frag) {
     float best_v;
     int best_e;
-    route_partial<DIM, NPT>(cur, s_g, s_b, s_br, g, 0, frag, best_v, best_e);
+    route_partial<DIM, NPT>(cur, s_br, g, 0, frag, best_v, best_e);
     if (best_e >= n_experts || best_e < 0) best_e = 0; /* non-finite logits */
     return best_e;
 }

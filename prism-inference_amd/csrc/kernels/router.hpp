@@ -43,7 +43,7 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
     constexpr int MAXTOK = 4 * ROUTER_MAX_TILES_PER_WAVE * 16;
     __shared__ int hist[64];
     __shared__ int base[64];
-    __shared__ float s_g[DIM], s_b[DIM], s_br[16 * NPT];
+    __shared__ float s_br[16 * NPT];
     __shared__ __attribute__((aligned(16))) h8 s_wr[NF * 64]; /* fragment-ordered W_r */
     __shared__ int s_e[MAXTOK], s_rank[MAXTOK];
 
@@ -63,10 +63,6 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
         for (int i = threadIdx.x; i < NF * 64; i += 256) s_wr[i] = src_r.load(i / 64, (i % 64) * 16);
     }
     if (threadIdx.x < 64) hist[threadIdx.x] = 0;
-    for (int i = threadIdx.x; i < DIM; i += 256) {
-        s_g[i] = a.ln_g[i];
-        s_b[i] = a.ln_b[i];
-    }
     for (int i = threadIdx.x; i < 16 * NPT; i += 256) s_br[i] = a.br[i];
     __syncthreads();
 
@@ -79,7 +75,7 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
         for (int ks = 0; ks < KS; ++ks) cur[ks] = xr[ks];
         if (it + 1 < tpw) router_load_tile<DIM, KS>(a, token + 16, g, xr); /* next tile in flight */
 
-        const int best_e = route_token<DIM, NPT>(cur, s_g, s_b, s_br, g, a.n_experts,
+        const int best_e = route_token<DIM, NPT>(cur, s_br, g, a.n_experts,
                                                  [&](int rt, int ks) { return s_wr[(rt * KS + ks) * 64 + lane]; });
         if (g == 0) {
             s_e[local] = best_e;
