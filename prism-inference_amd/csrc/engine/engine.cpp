@@ -223,6 +223,11 @@ struct BlockPlan {
 
 inline int round16(int n) { return (n + 15) & ~15; }
 
+/* Tokens in one launch: the counting sort's int32 slots, and the kernels
+ * address a launch's rows with 32-bit byte offsets (as the reference's
+ * shaders do), so its activations stay under 4 GiB. */
+inline bool tokens_fit(int64_t n, int dim) { return n <= 0x7fffffff / 64 && n * dim * 2 <= 0xffffffffll; }
+
 }  // namespace
 
 extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const void* blob, size_t bytes,
@@ -608,6 +613,8 @@ static int check_attn(prism_ctx* c, const prism_attn_push* p, void* features, in
     if (p->n_tokens < ATTN_MIN_TOKENS)
         return fail(c, PRISM_ERR_UNSUPPORTED, "%d tokens per frame: attention needs at least %d (%s)", p->n_tokens,
                     ATTN_MIN_TOKENS, ATTN_MIN_TOKENS_WHY);
+    if (!tokens_fit(p->n_tokens, p->dim)) /* a frame's rows, addressed with 32-bit offsets */
+        return fail(c, PRISM_ERR_INVALID, "%d tokens per frame is too many", p->n_tokens);
     const DevBlock* k = find_block(c, p->qkv_w, 0);
     if (!k || k->offs.qkv_b != p->qkv_b || k->offs.out_w != p->out_w || k->offs.out_b != p->out_b ||
         k->offs.ln1_g != p->ln1_g || k->offs.ln1_b != p->ln1_b)
@@ -631,7 +638,7 @@ static int check_router(prism_ctx* c, const prism_router_push* p, const void* fe
     if (p->dim != c->desc.dim || p->n_experts != c->desc.n_experts)
         return fail(c, PRISM_ERR_INVALID, "push dim=%d n_experts=%d does not match the loaded model", p->dim, p->n_experts);
     const int64_t n = (int64_t)batch * p->n_tokens;
-    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    if (!tokens_fit(n, c->desc.dim)) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
     const DevBlock* k = find_block(c, p->router_w, 1);
     if (!k || k->offs.router_b != p->router_b || k->offs.ln2_g != p->ln2_g || k->offs.ln2_b != p->ln2_b)
         return fail(c, PRISM_ERR_INVALID, "router weight offsets do not name a loaded block");
@@ -734,7 +741,7 @@ extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* fea
     if (!dense && (!aux || p->perm_offset < 0))
         return fail(c, PRISM_ERR_INVALID, "routed expert stage needs aux with count and perm regions");
     const int64_t n = (int64_t)batch * p->n_tokens;
-    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    if (!tokens_fit(n, c->desc.dim)) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
     const DevBlock* k = find_block(c, p->w1, 2);
     if (!k || k->offs.exp_b1 != p->b1 || k->offs.exp_w2 != p->w2 || k->offs.exp_b2 != p->b2 ||
         k->offs.exp_stride != p->expert_stride || k->offs.ln2_g != p->ln2_g || k->offs.ln2_b != p->ln2_b)
@@ -817,7 +824,7 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
     drop_graph(c);
     drop_workspace(c);
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
-    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    if (!tokens_fit(n, c->desc.dim)) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
     const ChainLayout L = chain_layout(c->desc, n, io);
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, L.bytes);
@@ -1055,7 +1062,7 @@ extern "C" int prism_forward_noalloc(prism_ctx* c, const void* in, void* out, in
     if (rc) return rc;
     if (!c->scratch) return fail(c, PRISM_ERR_STATE, "no scratch array on device %d", c->device);
     const int64_t n = (int64_t)batch * c->desc.spatial_h * c->desc.spatial_w;
-    if (n > 0x7fffffff / 64) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
+    if (!tokens_fit(n, c->desc.dim)) return fail(c, PRISM_ERR_INVALID, "%lld tokens is too many", (long long)n);
     const ChainLayout L = chain_layout(c->desc, n, false);
     if (L.bytes > PRISM_SCRATCH_BYTES)
         return fail(c, PRISM_ERR_INVALID,

@@ -51,7 +51,8 @@ bool shape_supported(const prism_model_desc* d, std::string* why) {
         if (why) *why = buf;
         return false;
     }
-    if (d->spatial_h < 1 || d->spatial_w < 1 || (int64_t)d->spatial_h * d->spatial_w > (1 << 24)) {
+    if (d->spatial_h < 1 || d->spatial_w < 1 || (int64_t)d->spatial_h * d->spatial_w > (1 << 24) ||
+        (int64_t)d->spatial_h * d->spatial_w * d->dim * 2 > 0xffffffffll) { /* a frame's rows under 4 GiB */
         snprintf(buf, sizeof buf, "token grid %dx%d out of range", d->spatial_h, d->spatial_w);
         if (why) *why = buf;
         return false;

@@ -238,18 +238,34 @@ struct RowChunk {
     h8 a0, a1;
 };
 
+/* 16 bytes at byte offset `off` of a row tensor. The host keeps every
+ * launch's rows under 4 GiB (the reference's 32-bit byte offsets), so the
+ * offset is a 32-bit unsigned VGPR and the compiler uses the SGPR-base +
+ * VGPR-offset global addressing form: no 64-bit address arithmetic. */
+__device__ __forceinline__ h8 ld_row16(const uint16_t* base, uint32_t off) {
+    return *reinterpret_cast<const h8*>(reinterpret_cast<const unsigned char*>(base) + off);
+}
+__device__ __forceinline__ void st_row16(uint16_t* base, uint32_t off, h8 v) {
+    *reinterpret_cast<h8*>(reinterpret_cast<unsigned char*>(base) + off) = v;
+}
+
 /* The caller passes an in-bounds row also for a padded or absent row (its
  * values are then never used: ln_store writes zeros for it and its raw copy
  * is never stored), so the load needs no zero fill and no branch. */
 template <int DIM>
-__device__ __forceinline__ RowChunk ln_load(const uint16_t* row) {
+__device__ __forceinline__ RowChunk ln_load(const uint16_t* base, uint32_t row) {
     constexpr int LPS = DIM / 16;
-    const int ca = (lane_id() % LPS) * 8, cb = ca + DIM / 2;
-    return RowChunk{*reinterpret_cast<const h8*>(row + ca), *reinterpret_cast<const h8*>(row + cb)};
+    const uint32_t ca = (lane_id() % LPS) * 8;
+    const uint32_t off = (row * DIM + ca) * 2u;
+    return RowChunk{ld_row16(base, off), ld_row16(base, off + DIM)};
 }
 
-/* ZERO = false: the caller never uses an invalid row's output (its GEMM
- * column is never stored), so it is left as computed from the stand-in row. */
+/* ZERO: an invalid row (padded window slot) is written as zeros, through
+ * inv = nmi = 0, which gives +0 for every finite stand-in value; the
+ * attention kernel's stand-in is its window's slot 0, so a non-finite one
+ * only reaches a window whose every output is already NaN. ZERO = false:
+ * the caller never uses an invalid row's output (its GEMM column is never
+ * stored), so it is left as computed from the stand-in row. */
 template <int DIM, bool ZERO = true>
 __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, f16* dst, f16* raw_dst) {
     constexpr int LPS = DIM / 16;
@@ -264,8 +280,12 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, f16* ds
     s = group_sum<LPS>(s);
     q = group_sum<LPS>(q);
     float mean;
-    const float inv = ln_inv<DIM>(s, q, mean);
-    const float nmi = -mean * inv;
+    float inv = ln_inv<DIM>(s, q, mean);
+    float nmi = -mean * inv;
+    if constexpr (ZERO) { /* an invalid row normalises to +0 (its stand-in row is finite or its window is NaN anyway) */
+        inv = valid ? inv : 0.f;
+        nmi = valid ? nmi : 0.f;
+    }
     h8 o0, o1;
 #pragma unroll
     for (int j = 0; j < 8; j += 4) {
@@ -280,12 +300,6 @@ __device__ __forceinline__ void ln_store(const RowChunk& rc, bool valid, f16* ds
             o1[j + i] = p1[i];
         }
     }
-    /* with ZERO, padded / missing rows are zero: select on whole 32-bit words */
-    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
-    u4 w0 = __builtin_bit_cast(u4, o0), w1 = __builtin_bit_cast(u4, o1);
-    const unsigned int keep = (valid || !ZERO) ? 0xffffffffu : 0u;
-    w0 &= keep;
-    w1 &= keep;
-    *reinterpret_cast<h8*>(dst + ca) = __builtin_bit_cast(h8, w0);
-    *reinterpret_cast<h8*>(dst + cb) = __builtin_bit_cast(h8, w1);
+    *reinterpret_cast<h8*>(dst + ca) = o0;
+    *reinterpret_cast<h8*>(dst + cb) = o1;
 }

@@ -58,7 +58,7 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
         const int c8 = (lane % CPR) * 8;
         const int tk = tok[r];
         if (tk >= 0)
-            *reinterpret_cast<h8*>(out + (int64_t)tk * C + c8) = *reinterpret_cast<const h8*>(tile + r * STRIDE + c8);
+            st_row16(out, ((uint32_t)tk * C + c8) * 2u, *reinterpret_cast<const h8*>(tile + r * STRIDE + c8));
     }
 }
 
@@ -158,7 +158,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-            rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM); /* none: row 0 */
+            rc[it] = ln_load<DIM>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
         }
         h8 wf[RT][KS];
 #pragma unroll
@@ -410,7 +410,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-        rc[it] = ln_load<DIM>(a.in + (int64_t)(rt_tok[it] >= 0 ? rt_tok[it] : 0) * DIM); /* none: row 0 */
+        rc[it] = ln_load<DIM>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
     }
     h8 ring[PF];
 #pragma unroll
@@ -465,7 +465,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
         const int tk = tok[wave * (BM / NW) + it * RPS + lane / CPR];
-        hx[it] = *reinterpret_cast<const h8*>(a.in + (int64_t)(tk >= 0 ? tk : 0) * DIM + c8); /* none: row 0, unused */
+        hx[it] = ld_row16(a.in, ((uint32_t)(tk >= 0 ? tk : 0) * DIM + c8) * 2u); /* none: row 0, unused */
     }
 #pragma unroll
     for (int r = 0; r < RT; ++r)
@@ -484,8 +484,8 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
         const int r = wave * (BM / NW) + it * RPS + lane / CPR;
         const int tk = tok[r];
         if (tk >= 0)
-            *reinterpret_cast<h8*>(a.out + (int64_t)tk * DIM + c8) =
-                add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]);
+            st_row16(a.out, ((uint32_t)tk * DIM + c8) * 2u,
+                     add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]));
     }
 }
 
