@@ -190,7 +190,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         for (int it = 0; it < IT; ++it) {
             const int s = wave * SPW + it * SPI + lane / LPS;
             const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-            rc[it] = ln_load<DIM>(in, valid[it] ? gy * a.W + gx : wy * 8 * a.W + wxx * 8); /* padded: slot 0's row */
+            rc[it] = ln_load<DIM, NW == 8>(in, valid[it] ? gy * a.W + gx : wy * 8 * a.W + wxx * 8); /* padded: slot 0's row */
         }
     } else {
 #pragma unroll
@@ -594,7 +594,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             const int c8 = (lane % CPR) * 8;
             const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
             if (gy < a.H && gx < a.W)
-                st_row16(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u,
+                st_row16<NW == 8>(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u,
                          *reinterpret_cast<const h8*>(os + sl * LDS + c8));
         }
     }

@@ -47,7 +47,7 @@
  * halfs) to the rows of its tokens: each wave stores BM/NW rows, 16 bytes
  * per lane, so one instruction covers 1 KiB of whole rows instead of 16
  * tokens x 32 bytes. */
-template <int C, int STRIDE, int BM, int NW>
+template <int C, int STRIDE, int BM, int NW, bool NT = false>
 __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile, const int* tok, int wave, int lane) {
     constexpr int CPR = C / 8;    /* 16-byte chunks per row */
     constexpr int RPS = 64 / CPR; /* rows per wave store    */
@@ -58,7 +58,7 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
         const int c8 = (lane % CPR) * 8;
         const int tk = tok[r];
         if (tk >= 0)
-            st_row16(out, ((uint32_t)tk * C + c8) * 2u, *reinterpret_cast<const h8*>(tile + r * STRIDE + c8));
+            st_row16<NT>(out, ((uint32_t)tk * C + c8) * 2u, *reinterpret_cast<const h8*>(tile + r * STRIDE + c8));
     }
 }
 
@@ -158,7 +158,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-            rc[it] = ln_load<DIM>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
+            rc[it] = ln_load<DIM, NW == 8>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
         }
         h8 wf[RT][KS];
 #pragma unroll
@@ -267,7 +267,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             }
         __syncthreads();
         if (!dn) {
-            expert_store_rows<DIM, LDS, BM, NW>(a.out, hs, tok, wave, lane);
+            expert_store_rows<DIM, LDS, BM, NW, NW == 8>(a.out, hs, tok, wave, lane);
         } else {
             /* r16(W_dn y + b_dn) (shaders/pw_project_256to128.comp.glsl:25-32,
              * the same arithmetic as prism_project_down_d*) from the output
@@ -295,7 +295,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
                     *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + (wave * DRT + r) * 16 + 4 * g) =
                         cvt_h4(dacc[r][t]);
             __syncthreads();
-            expert_store_rows<DO, LDS, BM, NW>(a.out, xs, tok, wave, lane);
+            expert_store_rows<DO, LDS, BM, NW, NW == 8>(a.out, xs, tok, wave, lane);
         }
     }
 
