@@ -452,6 +452,52 @@ int oracle_conv3x3(const float* x, int cin, int h, int w, int stride, const floa
     return rc;
 }
 
+/* The reference's split strided convs, with their own rounding (ReLU and
+ * stride 2 as in those shaders, padding 1): the input channels go in G groups
+ * of gc = cin / G, and each group's partial p_g = r16(b + W[:, g*9gc ..
+ * (g+1)*9gc) . x_g) is the shader's coopVecMatMulAddNV fp16 result.
+ *   mode 0, strided_conv_split_64ch.comp.glsl:49-92 (G = 2): v = (p_0 + p_1)
+ *     - b in fp32, y = r16(ReLU(v));
+ *   mode 1, strided_conv_split_128ch.comp.glsl:47-94: acc = p_0, then
+ *     acc = r16((acc + p_g) - b) for g = 1 .. G-1, y = ReLU(acc).
+ * The build's kernels (and oracle_conv3x3) round the unsplit sum once; this
+ * function is what that is compared against to bound the difference. */
+int oracle_conv3x3_split(const float* x, int cin, int h, int w, const float* W, const float* b, int cout, int groups,
+                         int mode, float* y) {
+    if (!x || !W || !b || !y || cin <= 0 || cout <= 0 || h <= 0 || w <= 0 || groups <= 0 || cin % groups ||
+        (mode != 0 && mode != 1) || (mode == 0 && groups != 2))
+        return -1;
+    const int gc = cin / groups, K = cin * 9, Kg = gc * 9;
+    const int oh = (h - 1) / 2 + 1, ow = (w - 1) / 2 + 1;
+    const size_t n = (size_t)cout * oh * ow;
+    float* Wg = (float*)malloc(sizeof(float) * (size_t)cout * Kg);
+    float* part = (float*)malloc(sizeof(float) * n);
+    if (!Wg || !part) {
+        free(Wg);
+        free(part);
+        return -2;
+    }
+    int rc = 0;
+    for (int g = 0; g < groups && !rc; ++g) {
+        for (int o = 0; o < cout; ++o) memcpy(Wg + (size_t)o * Kg, W + (size_t)o * K + (size_t)g * Kg, sizeof(float) * Kg);
+        rc = oracle_conv3x3(x + (size_t)g * gc * h * w, gc, h, w, 2, Wg, b, cout, 0, 1, part);
+        if (rc) break;
+        for (size_t i = 0; i < n; ++i) {
+            const float bb = b[i / ((size_t)oh * ow)];
+            if (g == 0) y[i] = part[i];
+            else if (mode == 0) y[i] = (y[i] + part[i]) - bb; /* fp32, rounded below */
+            else y[i] = r16((y[i] + part[i]) - bb);
+        }
+    }
+    for (size_t i = 0; i < n && !rc; ++i) {
+        const float v = y[i] < 0.f ? 0.f : y[i];
+        y[i] = mode == 0 ? r16(v) : v;
+    }
+    free(Wg);
+    free(part);
+    return rc;
+}
+
 /* Fused decoder stage (dec3_fused.comp.glsl:27-63, dec{2,1}_fused.comp.glsl:
  * 27-55): in = concat(up[c][min(oy/2, uh-1)][min(ox/2, uw-1)] for c < cup,
  * skip[c][oy][ox] for c < cskip); y[o][oy][ox] = ReLU(r16(W[o] . in + b[o])).

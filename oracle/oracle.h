@@ -99,6 +99,11 @@ int oracle_project(const float* W, const float* b, int in_dim, int out_dim, int 
 /* Encoder / decoder stages on CHW maps (oracle.c has the formulas). */
 int oracle_conv3x3(const float* x, int cin, int h, int w, int stride, const float* W, const float* b, int cout,
                    int relu, int faithful, float* y);
+/* The reference's split strided convs with their per-group fp16 rounding
+ * (mode 0: two groups combined in fp32, the 64-channel shader; mode 1: a
+ * running fp16 sum, the 128-channel shader); stride 2, ReLU. */
+int oracle_conv3x3_split(const float* x, int cin, int h, int w, const float* W, const float* b, int cout, int groups,
+                         int mode, float* y);
 int oracle_dec_stage(const float* up, int cup, int uh, int uw, const float* skip, int cskip, int oh, int ow,
                      const float* W, const float* b, int cout, int faithful, float* y);
 int oracle_pw_conv(const float* x, int cin, int h, int w, const float* W, const float* b, int cout, int relu,

@@ -51,6 +51,7 @@ def lib():
         L.oracle_project.argtypes = [_F, _F, C.c_int, C.c_int, C.c_int, _F, C.c_int, C.c_int, _F]
         L.oracle_window_attention.argtypes = [C.POINTER(Cfg), _F, _F, _F, _F]
         L.oracle_conv3x3.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int, _F]
+        L.oracle_conv3x3_split.argtypes = [_F, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int, _F]
         L.oracle_dec_stage.argtypes = [_F, C.c_int, C.c_int, C.c_int, _F, C.c_int, C.c_int, C.c_int, _F, _F,
                                        C.c_int, C.c_int, _F]
         L.oracle_pw_conv.argtypes = [_F, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int, _F]
@@ -212,6 +213,20 @@ def conv3x3(x: np.ndarray, W: np.ndarray, b: np.ndarray, stride: int, relu: bool
     y = np.empty((cout, oh, ow), np.float32)
     _chk(lib().oracle_conv3x3(_f(x), cin, h, w, stride, _f(W), _f(b), cout, int(relu), int(faithful), _f(y)),
          "oracle_conv3x3")
+    return y
+
+
+def conv3x3_split(x: np.ndarray, W: np.ndarray, b: np.ndarray, groups: int, mode: int) -> np.ndarray:
+    """The reference's split stride-2 conv3x3 + ReLU with its own rounding: each
+    group's partial sum r16(b + W_g . x_g), combined in fp32 (mode 0, two
+    groups: strided_conv_split_64ch) or as a running fp16 sum (mode 1:
+    strided_conv_split_128ch). x [cin][h][w], W [cout][cin*9]."""
+    cin, h, w = x.shape
+    cout = W.shape[0]
+    x, W, b = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, W, b))
+    y = np.empty((cout, (h - 1) // 2 + 1, (w - 1) // 2 + 1), np.float32)
+    _chk(lib().oracle_conv3x3_split(_f(x), cin, h, w, _f(W), _f(b), cout, groups, mode, _f(y)),
+         "oracle_conv3x3_split")
     return y
 
 

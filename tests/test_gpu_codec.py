@@ -85,6 +85,12 @@ def test_codec_stages_teacher_forced(hip, engine, device_arena, render):
         ref["e" + str(st)] = O.conv3x3(x, *W(name), stride=2)
         got = run_stage(hip, engine, device_arena, st, nhwc(x), None, ho * wo * cout)
         checks.append((name, chw(got, ho, wo), ref["e" + str(st)]))
+        if name in ("enc2", "enc3"):
+            # the reference's split convs round each 288-column partial sum
+            # (strided_conv_split_{64,128}ch.comp.glsl); this build rounds the
+            # whole sum once: both within the block tolerance of each other
+            split = O.conv3x3_split(x, *W(name), groups=cin // 32, mode=0 if cin == 64 else 1)
+            checks.append((name + " vs split rounding", chw(got, ho, wo), split))
     # decoder: coarse input = a synthetic ReLU-like map, skips = the encoder maps
     up3 = np.maximum(f16(rng.standard_normal((128, h3, w3))), 0)
     d3 = O.dec_stage(up3, ref["e2"], *W("dec3"))
@@ -131,7 +137,12 @@ def test_encode_decode_against_the_oracle_chain(hip, engine, device_arena):
         e3 = O.conv3x3(e2, *W("enc3"), stride=2)
         mx, mean = errors(chw(bott[f * h3 * w3 * 128:(f + 1) * h3 * w3 * 128], h3, w3), e3)
         print(f"[codec] frame {f} bottleneck: max {mx:.3g} mean {mean:.3g}", flush=True)
-        assert mx <= 4 * MAX_ABS and mean <= MEAN_ABS
+        assert mx <= MAX_ABS and mean <= MEAN_ABS
+        # the same chain with the reference's split-conv rounding in enc2/enc3
+        s3 = O.conv3x3_split(O.conv3x3_split(e1, *W("enc2"), groups=2, mode=0), *W("enc3"), groups=4, mode=1)
+        mx, mean = errors(chw(bott[f * h3 * w3 * 128:(f + 1) * h3 * w3 * 128], h3, w3), s3)
+        print(f"[codec] frame {f} bottleneck vs split rounding: max {mx:.3g} mean {mean:.3g}", flush=True)
+        assert mx <= MAX_ABS and mean <= MEAN_ABS
         d3 = O.dec_stage(z[f], e2, *W("dec3"))
         d2 = O.dec_stage(d3, e1, *W("dec2"))
         d1 = O.dec_stage(d2, e0, *W("dec1"))

@@ -138,3 +138,70 @@ def test_pixelshuffle_sigmoid_matches_torch():
     logit = np.log(g64 / (1 - g64))  # fp32 sigmoid near 1 keeps ~1e-4 of the logit
     back = F.pixel_unshuffle(torch.from_numpy(logit)[None], 2)[0].numpy()
     assert np.abs(back - x).max() <= 2e-3
+
+
+# ---- the reference's split strided convs (their own per-group rounding) ----
+
+def torch_split(x, W, b, groups, mode):
+    """strided_conv_split_{64,128}ch restated with torch fp64 group convs: each
+    group's partial rounded to fp16 with its bias, combined in fp32 (mode 0)
+    or as a running fp16 sum (mode 1), then ReLU. Also returns the largest
+    |partial| per element (the scale of a one-ulp flip of a partial)."""
+    gc = x.shape[0] // groups
+    parts = [r16(torch_conv(x[g * gc:(g + 1) * gc], W[:, g * gc * 9:(g + 1) * gc * 9], b, 2, False))
+             for g in range(groups)]
+    scale = np.max(np.abs(np.stack(parts)), axis=0)
+    bb = b.astype(np.float32)[:, None, None]
+    if mode == 0:
+        v = (parts[0].astype(np.float32) + parts[1].astype(np.float32)) - bb
+        return r16(np.maximum(v, 0)), scale
+    acc = parts[0]
+    for g in range(1, groups):
+        acc = r16((acc.astype(np.float32) + parts[g].astype(np.float32)) - bb)
+        scale = np.maximum(scale, np.abs(acc))
+    return np.maximum(acc, 0), scale
+
+
+@pytest.mark.parametrize("cin,groups,mode", [(64, 2, 0), (128, 4, 1), (64, 2, 1)])
+def test_conv3x3_split_matches_torch_restatement(cin, groups, mode):
+    x = f16(rng.standard_normal((cin, 11, 13)))
+    W = f16(rng.standard_normal((128, cin * 9)) * 0.05)
+    b = f16(rng.standard_normal(128) * 0.05)
+    got = O.conv3x3_split(x, W, b, groups, mode)
+    ref, scale = torch_split(x, W, b, groups, mode)
+    assert got.shape == ref.shape == (128, 6, 7)
+    # identical except where an fp32 (oracle) and an fp64 (torch) partial sum
+    # round to neighbouring fp16 values: one ulp of that partial, rarely
+    d = np.abs(got - ref)
+    ulp = np.maximum(np.maximum(np.abs(ref), scale) * 2.0 ** -10, 2.0 ** -24)
+    assert (d <= groups * ulp + 1e-7).all() and (d > 0).mean() < 0.01
+    # and the unsplit conv (this build's single rounding) is within a few ulps
+    one = O.conv3x3(x, W, b, 2, relu=True, faithful=True)
+    assert (np.abs(one - got) <= (groups + 1) * np.maximum(scale, np.abs(ref)) * 2.0 ** -10 + 1e-7).all()
+
+
+def test_conv3x3_split_one_group_is_the_unsplit_conv():
+    x = f16(rng.standard_normal((32, 9, 10)))
+    W = f16(rng.standard_normal((64, 32 * 9)) * 0.05)
+    b = f16(rng.standard_normal(64) * 0.05)
+    np.testing.assert_array_equal(O.conv3x3_split(x, W, b, 1, 1), O.conv3x3(x, W, b, 2, relu=True, faithful=True))
+
+
+@pytest.mark.parametrize("cin,groups,mode", [(64, 2, 0), (128, 4, 1)])
+def test_conv3x3_split_later_groups_zero(cin, groups, mode):
+    """With zero weights in groups 1.. and zero bias, every later partial is 0
+    and the result is group 0's conv with one rounding, exactly."""
+    x = f16(rng.standard_normal((cin, 12, 9)))
+    W = f16(rng.standard_normal((96, cin * 9)) * 0.05)
+    W[:, 32 * 9:] = 0
+    b = np.zeros(96, np.float32)
+    got = O.conv3x3_split(x, W, b, groups, mode)
+    np.testing.assert_array_equal(got, O.conv3x3(x[:32], W[:, :32 * 9], b, 2, relu=True, faithful=True))
+
+
+def test_conv3x3_split_rejects_bad_shapes():
+    x = np.zeros((48, 5, 5), np.float32)
+    with pytest.raises(Exception):
+        O.conv3x3_split(x, np.zeros((16, 48 * 9), np.float32), np.zeros(16, np.float32), 4, 0)  # mode 0: 2 groups
+    with pytest.raises(Exception):
+        O.conv3x3_split(x, np.zeros((16, 48 * 9), np.float32), np.zeros(16, np.float32), 5, 1)  # 48 % 5
