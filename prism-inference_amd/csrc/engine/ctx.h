@@ -46,7 +46,12 @@ static constexpr int CHAIN_SPLIT_FRAMES = 2;
 static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
 /* d256 expert launches of at least this many 128-token tiles (two per CU)
  * use the 128-token kernel: each streamed weight fragment then feeds twice
- * the tokens. Smaller grids keep 64-token tiles (8 waves below 512 tiles). */
+ * the tokens. Smaller grids keep 64-token tiles (8 waves below 512 tiles).
+ * A stage call of that size uses 96-token tiles of the same body instead:
+ * alone on the GPU, its last round of workgroups is then less empty (batch 8
+ * to 16 at 68x120: 7-13 % faster); inside the block chain the other
+ * sub-chain's attention launch fills that round, and 128-token tiles stay
+ * ahead there. */
 static constexpr int EXPERT_WIDE_MIN_TILES = 512;
 
 /* Attention keys all 64 slots of a window. The reference keys the first
@@ -76,6 +81,7 @@ struct prism_ctx {
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
     hipFunction_t f_expert_wide = nullptr; /* d256, 128-token tiles */
+    hipFunction_t f_expert_wide96 = nullptr; /* d256, 96-token tiles (large stage calls) */
     hipFunction_t f_zero = nullptr;
     hipFunction_t f_take = nullptr;
     hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */

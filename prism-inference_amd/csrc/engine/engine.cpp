@@ -102,7 +102,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_router[1][2], "prism_router_d256_n3"}, {&c->f_router[1][3], "prism_router_d256_n4"},
         {&c->f_expert[0][0], "prism_expert_d128_bm64"},  {&c->f_expert[1][0], "prism_expert_d256_bm64"},
         {&c->f_expert[0][1], "prism_expert_d128_bm64_w8"}, {&c->f_expert[1][1], "prism_expert_d256_bm64_w8"},
-        {&c->f_expert_wide, "prism_expert_d256_bm128"},
+        {&c->f_expert_wide, "prism_expert_d256_bm128"}, {&c->f_expert_wide96, "prism_expert_d256_bm96"},
         {&c->f_zero, "prism_zero_i32"}, {&c->f_take, "prism_take_counts"},
         {&c->f_proj[0][0], "prism_project_up_d128"},   {&c->f_proj[0][1], "prism_project_down_d128"},
         {&c->f_proj[1][0], "prism_project_up_d256"},   {&c->f_proj[1][1], "prism_project_down_d256"},
@@ -542,7 +542,8 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
 }
 
 int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, const int32_t* counts,
-                    const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1, bool dn = false) {
+                    const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1, bool dn = false,
+                    bool stage = false) {
     const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
     ExpertArgs a{};
     if (dn) { /* the adapted chain's last block: 128-channel output rows */
@@ -565,7 +566,8 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
      * a multiple of 8 (the kernels' XCD-major tile order) */
     auto tiles_of = [&](int64_t bm) { return ((n + bm - 1) / bm + (counts ? N : 0) + 7) / 8 * 8; };
     if (D == 256 && !dn && tiles_of(128) >= EXPERT_WIDE_MIN_TILES)
-        return launch(c, c->f_expert_wide, (unsigned)tiles_of(128), a, s, 256u);
+        return stage ? launch(c, c->f_expert_wide96, (unsigned)tiles_of(96), a, s, 256u)
+                     : launch(c, c->f_expert_wide, (unsigned)tiles_of(128), a, s, 256u);
     const int64_t tiles = tiles_of(64);
     /* fewer tiles than two per CU: 8 waves per tile halve each wave's weight stream */
     const int w8 = tiles < 512 ? 1 : 0;
@@ -752,7 +754,7 @@ extern "C" int prism_experts(prism_ctx* c, const prism_expert_push* p, void* fea
         return fail(c, PRISM_ERR_INVALID, "feature offsets must be multiples of 8 elements");
     HIP_TRY(c, hipSetDevice(c->device));
     return enqueue_experts(c, *k, f + p->input_offset, f + p->output_offset, dense ? nullptr : aux + p->count_offset,
-                           dense ? nullptr : aux + p->perm_offset, n, (hipStream_t)stream);
+                           dense ? nullptr : aux + p->perm_offset, n, (hipStream_t)stream, 1, false, true);
 }
 
 static int project_stage(prism_ctx* c, bool up, const prism_project_push* p, void* features, int32_t batch,

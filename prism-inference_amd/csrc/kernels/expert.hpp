@@ -34,10 +34,10 @@
  * unpermute; one store instruction covers two rows instead of 16 tokens x
  * 32 bytes).
  *
- * Two tile sizes: expert_body (64 tokens, 4 or 8 waves; the weight-streaming
- * scheme above) and expert_body_wide (128 tokens, 4 waves, d256, for large
- * grids: a weight ring instead of per-pass registers, the residual read
- * again instead of kept in LDS; see its comment). Both share the scheduler
+ * Tile sizes: expert_body (64 tokens, 4 or 8 waves; the weight-streaming
+ * scheme above) and expert_body_wide (128 or 96 tokens, 4 waves, d256, for
+ * large grids: a weight ring instead of per-pass registers, the residual read
+ * again instead of kept in LDS; see its comment). All share the scheduler
  * and give bit-identical results.
  */
 #pragma once
@@ -358,16 +358,19 @@ __device__ __forceinline__ void expert_wide_gemm(f4 (&acc)[RT][TT], h8 (&ring)[P
  * still feeds 4 MFMAs (one per row tile of the wave). The wave's weights
  * (W1's 64 rows, then W2's) stream through a ring of PF fragments, k-step-
  * major, so W2's first fragments are in flight during the GELU. The LDS holds
- * one 128-row tile (LN2 output, then GELU output, then y) and not the
- * residual: the tile's input rows (L2-resident since the gather) are read
- * again as GEMM2 ends and added to y as whole rows, 16 bytes per lane.
+ * one BM-row tile (LN2 output, then GELU output, then y) and not the
+ * residual: the tile's input rows are read again as GEMM2 ends (by then most
+ * have left the XCD's 4 MB L2, so this is a second fetch from the memory
+ * side) and added to y as whole rows, 16 bytes per lane. The same body at
+ * BM = 96 (6 token tiles) serves large stage calls, whose tile count then
+ * leaves less of a last, partly filled round of workgroups.
  * Per output element the arithmetic and its order are those of expert_body
  * (bias in the accumulator, k-steps in order, the same rounding points), so
  * the results are bit-identical to the 64-token kernels.
  */
-template <int DIM, int PF>
+template <int DIM, int PF, int BM>
 __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
-    constexpr int BM = 128, NW = 4, NT = 64 * NW;
+    constexpr int NW = 4, NT = 64 * NW;
     constexpr int KS = DIM / 32;
     constexpr int LDS = DIM + 8;
     constexpr int TT = BM / 16;       /* token tiles                   */
@@ -506,5 +509,10 @@ extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d128_bm64_w8(E
 /* 128-token tiles, 4 waves, 2 workgroups per CU: the large grids of batched
  * launches (no fused down-projection) */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm128(ExpertArgs a) {
-    expert_body_wide<256, 12>(a);
+    expert_body_wide<256, 12, 128>(a);
+}
+/* 96-token tiles of the same body: a large stage call's tile count then
+ * rounds up to whole rounds of the CUs' workgroup slots with less idle tail */
+extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm96(ExpertArgs a) {
+    expert_body_wide<256, 12, 96>(a);
 }

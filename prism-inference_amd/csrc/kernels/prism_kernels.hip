@@ -6,7 +6,7 @@
  *   prism_attn_d{256,128}[_w8]                     attention stage (4 or 8 waves)
  *   prism_attn_d{256,128}[_w8]_r{1..4}             attention + fused routing
  *   prism_router_d{256,128}_n{1..4}                router + counting sort
- *   prism_expert_d{256,128}_bm64[_w8], _d256_bm128  grouped expert FFN
+ *   prism_expert_d{256,128}_bm64[_w8], _d256_bm{128,96}  grouped expert FFN
  *   prism_project_{up,down}_d{256,128}             projection adapters (128 <-> dim)
  *   prism_codec_enc{0..3}, prism_codec_dec{3,2}    conv encoder / fused decoder stages
  *   prism_codec_dec1_out                           dec1 + output conv + PixelShuffle + sigmoid

@@ -11,7 +11,10 @@ the C ABI, against the oracle.
   or more frames as two sub-chains of half the frames each, and every MoE block
   as one routed attention launch (prism_attn_route) plus one grouped expert
   launch (prism_experts). Calling those two entry points on half the batch
-  runs exactly the kernels the chain launches (same grid, same variant); each
+  runs the chain's attention kernels (same grid, same variant) and its expert
+  kernels, except that a stage call of 512 or more 128-token tiles takes
+  96-token tiles of the same body where the chain keeps 128-token ones (the
+  two are bit-identical: test_chain_matches_stage_calls at batch 16); each
   block's input is the oracle's, so every block is held to the per-block
   tolerances (max 2e-2, mean 2e-3) and exact routing on every token whose
   oracle top-1/top-2 logit gap is >= 1e-2. Counts and buckets are exact.
@@ -91,7 +94,7 @@ def test_config_chain_against_oracle(hip, engine, device_arena, name, batch, ker
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,batch", [
-    ("moe64", 2, 16),   # sub-chains of 8 frames: 1080-window prism_attn_d256_r4, 128-token expert tiles
+    ("moe64", 2, 16),   # sub-chains of 8 frames: 1080-window prism_attn_d256_r4, 96-token expert tiles
     ("moe32", 2, 4),    # sub-chains of 2 frames at 135x240: 1020-window prism_attn_d256_r2
     ("moe64", 16, 1),   # every block of the headline model at batch 1 (8-wave kernels)
 ])

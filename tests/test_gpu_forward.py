@@ -83,6 +83,7 @@ EXTRA = {
     ("moe24d128", 3, 68, 120, 1),
     ("moe24d128", 2, 68, 120, 4),
     ("moe64", 2, 68, 120, 16),     # sub-chains of 8 frames: 4-wave _r4, 128-token expert tiles
+                                   # (the stage calls: 96-token tiles of the same body)
     ("moe32", 2, 135, 240, 1),     # 510 windows, 8 waves, 2 router row tiles split over wave pairs
     ("moe32", 2, 135, 240, 4),     # sub-chains of 2 frames (1020 windows each): 4-wave _r2
     ("moe16", 2, 68, 120, 8),      # sub-chains of 4 frames (540 windows each): 4-wave _r1

@@ -172,8 +172,10 @@ def test_dense_ffn_stage(hip, engine, device_arena, name, H, W, batch):
 ])
 def test_experts_wide_tiles(hip, engine, device_arena, name, H, W, B):
     """A batch of 65,280 or more tokens gives the d256 expert launch 512 or
-    more 128-token tiles, so it runs the 128-token kernel; one frame alone runs
-    a 64-token kernel. Each token's routing and output must be bit-identical
+    more 128-token tiles, so the stage call runs the 96-token kernel (the
+    chain's launches of that size run the 128-token one: same body, pinned bit
+    for bit by test_chain_matches_stage_calls); one frame alone runs a 64-token
+    kernel. Each token's routing and output must be bit-identical
     between the two (same arithmetic per token), and the batch's outputs must
     match the oracle, teacher-forced with the GPU's routing, on a sample of
     tokens (the expert stage acts per token)."""
@@ -207,7 +209,7 @@ def test_experts_wide_tiles(hip, engine, device_arena, name, H, W, B):
     y1, assign1 = run(1, 3)
     assert (assign1 == assign[3 * T:4 * T]).all(), "routing of frame 3 differs"
     diff = int((y1 != y[3 * T:4 * T]).sum())
-    assert diff == 0, f"{diff} output values of frame 3 differ between the 128- and 64-token kernels"
+    assert diff == 0, f"{diff} output values of frame 3 differ between the 96- and 64-token kernels"
 
     rng = np.random.default_rng(0)
     idx = np.sort(np.concatenate([np.arange(256), rng.choice(B * T, 3840, replace=False)]))
