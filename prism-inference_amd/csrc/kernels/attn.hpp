@@ -36,6 +36,10 @@
  *     global atomic per present expert, bucket scatter). This replaces the
  *     router launch and its re-read of h.
  *
+ * Windows whose slots 32-63 are all padded (a grid's bottom window row with
+ * 4 or fewer rows) take a body that computes only token tiles 0 and 1 (HALF,
+ * below): the other tiles' keys and values are the bias alone.
+ *
  * Weight streaming: every wave reads one fixed sequence of 1 KiB weight
  * fragments (head A's QKV k-steps, head B's, the out-proj's, the router's) through a
  * register ring PF fragments deep, so loads run 2 k-steps ahead of the MFMAs
@@ -108,10 +112,20 @@ struct AttnLds {
 /* PAD: the window has padded slots and the block's LN1 beta is not zero, so
  * those slots' keys and values need the unfolded bias (a separate
  * instantiation keeps that code, and its branches, out of every other
- * window's instruction schedule). vmask bit s: slot s holds a token. */
-template <int DIM, int HD, int NW, int NPT, bool PAD>
+ * window's instruction schedule). vmask bit s: slot s holds a token.
+ * HALF (not with PAD): slots 32-63 are all padded (the bottom windows of a
+ * grid whose height leaves 4 or fewer rows in the last window row, e.g. 68
+ * rows), so token tiles 2 and 3 are never queries, never stored and never
+ * routed: only their keys and values are used, and those are the bias alone
+ * (the zero LN1 output adds nothing to the accumulator that starts at the
+ * bias). The body then computes Q, the softmax rows, O, the out-projection,
+ * LN1 and the routing for tiles 0 and 1 only; every stored value is
+ * computed as in the full body. */
+template <int DIM, int HD, int NW, int NPT, bool PAD, bool HALF = false>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM, NPT>& L,
                                                  unsigned long long vmask) {
+    static_assert(!(PAD && HALF), "HALF windows take the unpadded body");
+    constexpr int TQ = HALF ? 2 : 4; /* token tiles that hold tokens */
     static_assert(DIM / HD == 8, "8 heads");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(NPT >= 0 && NPT <= 4, "up to 64 experts");
@@ -157,8 +171,9 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     const FragSrc src_o(a.wo, 1u * DIM * DIM * 2u);
     const FragSrc src_r(NPT > 0 ? a.wr : a.wo, NPT > 0 ? 16u * NPT * DIM * 2u : 0u);
     const int loff = lane * 16;
-    /* waves 0-3 route tiles 0-3 of the window; only they stream W_r */
-    const bool routes = NPT > 0 && (S::RSPLIT || wave < 4);
+    /* waves 0-3 route tiles 0-3 of the window (waves w and w+4 tile w % 4
+     * when split); only they stream W_r */
+    const bool routes = NPT > 0 && (S::RSPLIT ? (wave & 3) < TQ : wave < TQ);
     const int total = routes ? S::TOTAL : S::RBASE;
 
     /* ---- 1. LN1 --------------------------------------------------------
@@ -175,6 +190,9 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     constexpr int UIN = 128, UKS = UIN / 32, UPR = DIM / 16 / NW, EPT = 64 * (UIN / 8) / NT;
     static_assert(UPR >= 1 && EPT >= 1, "up-projection shape");
     const bool up = a.up_w != nullptr; /* uniform over the launch */
+    /* HALF: the waves whose slots are all padded skip LN1 (their rows of xs
+     * and os are never read) */
+    const bool lnw = !HALF || wave * SPW < 16 * TQ;
     RowChunk rc[IT];
     bool valid[IT];
     h8 erow[EPT];
@@ -186,11 +204,13 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         valid[it] = gy < a.H && gx < a.W;
     }
     if (!up) {
+        if (lnw) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int s = wave * SPW + it * SPI + lane / LPS;
-            const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
-            rc[it] = ln_load<DIM, NW == 8>(in, valid[it] ? gy * a.W + gx : wy * 8 * a.W + wxx * 8); /* padded: slot 0's row */
+            for (int it = 0; it < IT; ++it) {
+                const int s = wave * SPW + it * SPI + lane / LPS;
+                const int gy = wy * 8 + (s >> 3), gx = wxx * 8 + (s & 7);
+                rc[it] = ln_load<DIM, NW == 8>(in, valid[it] ? gy * a.W + gx : wy * 8 * a.W + wxx * 8); /* padded: slot 0's row */
+            }
         }
     } else {
 #pragma unroll
@@ -228,10 +248,12 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
     __syncthreads(); /* parameters staged */
     if (!up) {
+        if (lnw) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
-            ln_store<DIM>(rc[it], valid[it], xs + row, os + row); /* os: the raw rows (residual) */
+            for (int it = 0; it < IT; ++it) {
+                const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+                ln_store<DIM>(rc[it], valid[it], xs + row, os + row); /* os: the raw rows (residual) */
+            }
         }
     } else {
         /* x = r16(ReLU(W_up e + b_up)) for the window's slots, the same
@@ -313,12 +335,12 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
          * k-step ks's MFMAs, so their latency hides behind them */
         h8 xf[4], xn[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
+        for (int t = 0; t < TQ; ++t) xf[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             if (ks + 1 < KS) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
+                for (int t = 0; t < TQ; ++t)
                     xn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
             }
 #pragma unroll
@@ -327,7 +349,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
                 const h8 w = ring[p % PF];
                 const int mat = f / CT, c = f % CT;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < TQ; ++t) {
                     if (mat == 0) accQ[c][t] = mfma_16x16x32(w, xf[t], accQ[c][t]);
                     else if (mat == 1) accK[c][t] = mfma_16x16x32(w, xf[t], accK[c][t]);
                     else accV[t][c] = mfma_16x16x32(xf[t], w, accV[t][c]);
@@ -337,7 +359,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             }
             if (ks + 1 < KS) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) xf[t] = xn[t];
+                for (int t = 0; t < TQ; ++t) xf[t] = xn[t];
             }
             sched_fence();
         }
@@ -388,7 +410,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         h4 p[4][4];
         float inv[4];
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
+        for (int qt = 0; qt < TQ; ++qt) {
             f4 s[4];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
@@ -419,7 +441,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         {
             const h8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt) {
+            for (int qt = 0; qt < TQ; ++qt) {
                 f4 z = f4_zero();
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
@@ -436,7 +458,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
 #pragma unroll
         for (int dt = 0; dt < CT; ++dt)
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt) {
+            for (int qt = 0; qt < TQ; ++qt) {
                 f4 o = f4_zero();
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
@@ -459,7 +481,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
 #pragma unroll
         for (int dt = 0; dt < CT; ++dt)
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt)
+            for (int qt = 0; qt < TQ; ++qt)
                 *reinterpret_cast<h4*>(xs + (16 * qt + l16) * LDS + (wave + NW * hh) * HD + 16 * dt + 4 * g) =
                     okeep[hh][dt][qt];
     if constexpr (NPT > 0) /* the QKV biases are dead now */
@@ -477,12 +499,12 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     }
     h8 of[4], on[4]; /* double-buffered like the QKV operands */
 #pragma unroll
-    for (int t = 0; t < 4; ++t) of[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
+    for (int t = 0; t < TQ; ++t) of[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < TQ; ++t)
                 on[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
         }
 #pragma unroll
@@ -490,18 +512,18 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             const int p = S::HPW * S::HEADF + ks * ORT + r;
             const h8 w = ring[p % PF];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
+            for (int t = 0; t < TQ; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
             if (p + PF < S::TOTAL && p + PF < total)
                 ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
         }
         if (ks + 1 < KS) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) of[t] = on[t];
+            for (int t = 0; t < TQ; ++t) of[t] = on[t];
         }
         sched_fence();
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TQ; ++t) {
         const int sl = 16 * t + l16;
 #pragma unroll
         for (int r = 0; r < ORT; ++r) {
@@ -530,18 +552,21 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             float* const r_pv = reinterpret_cast<float*>(xs);
             int* const r_pe = reinterpret_cast<int*>(xs) + 64;
             const int sl = 16 * (wave & 3) + l16;
-            h8 cur[KS];
+            float bv = 0.f;
+            int be = 0;
+            if (routes) {
+                h8 cur[KS];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
-            float bv;
-            int be;
-            route_partial<DIM, S::RPT>(cur, s_br, g, wave >= 4 ? S::RPT : 0, rfrag, bv, be);
-            if (wave >= 4 && g == 0) {
-                r_pv[sl] = bv;
-                r_pe[sl] = be;
+                for (int ks = 0; ks < KS; ++ks)
+                    cur[ks] = *reinterpret_cast<const h8*>(os + sl * LDS + 32 * ks + 8 * g);
+                route_partial<DIM, S::RPT>(cur, s_br, g, wave >= 4 ? S::RPT : 0, rfrag, bv, be);
+                if (wave >= 4 && g == 0) {
+                    r_pv[sl] = bv;
+                    r_pe[sl] = be;
+                }
             }
             __syncthreads();
-            if (wave < 4) {
+            if (wave < 4 && routes) {
                 float v;
                 int e;
                 route_pick(bv, be, r_pv[sl], r_pe[sl], v, e);
@@ -608,6 +633,8 @@ __device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>
     const unsigned long long vmask = __ballot(wy * 8 + (lane >> 3) < a.H && wxx * 8 + (lane & 7) < a.W);
     if (a.bqkv_pad != nullptr && vmask != ~0ull) /* uniform */
         attn_window_body<DIM, HD, NW, NPT, true>(a, L, vmask);
+    else if ((vmask >> 32) == 0ull && a.up_w == nullptr)
+        attn_window_body<DIM, HD, NW, NPT, false, true>(a, L, vmask);
     else
         attn_window_body<DIM, HD, NW, NPT, false>(a, L, vmask);
 }
