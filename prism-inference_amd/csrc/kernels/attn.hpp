@@ -239,14 +239,15 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     if (NPT > 0 && a.zero_next && blockIdx.x == 0 && threadIdx.x < a.n_experts)
         a.zero_next[threadIdx.x * a.count_stride] = 0;
     /* every parameter is staged now: a load issued after the residual
-     * prefetch below would make its LDS store wait for that HBM fetch */
+     * prefetch below would make its LDS store wait for that HBM fetch. The
+     * barrier after LN1 publishes them (each wave starts its LN1 as soon as
+     * its own rows are in, without waiting for the other waves' stores) */
     for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
     if constexpr (PAD)
         for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv_pad[i] = a.bqkv_pad[i];
     for (int i = threadIdx.x; i < DIM; i += NT) s_bo[i] = a.bo[i];
     if constexpr (NPT > 0)
         for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
-    __syncthreads(); /* parameters staged */
     if (!up) {
         if (lnw) {
 #pragma unroll

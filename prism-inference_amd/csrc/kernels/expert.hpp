@@ -12,10 +12,9 @@
  * rounded up to a multiple of 8). Workgroup i maps to logical tile
  * (i % 8) * (grid / 8) + i / 8 so that consecutive tiles of one expert land on
  * the same XCD (hardware dispatches workgroups round-robin over the 8 XCDs)
- * and share that XCD's L2 copy of the expert's weights. Wave 0 turns the
+ * and share that XCD's L2 copy of the expert's weights. Every wave turns the
  * per-expert counts into a tile prefix sum (a DPP scan) and finds its
- * (expert, row block);
- * tiles past the end do nothing.
+ * (expert, row block) itself; tiles past the end do nothing.
  *
  * Weight streaming: as soon as the tokens are gathered, each wave issues
  * every W1 fragment of its 16*RT output rows (RT*KS 1 KiB fragments, held in
@@ -62,34 +61,36 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
     }
 }
 
-/* Tile scheduler (see the file comment): wave 0 finds this workgroup's
- * (expert, first row, row count), or expert -1 past the last tile. The
- * caller synchronises. */
-template <int DIM, int BM, int NT>
-__device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int wave, int lane, int& sh_e, int& sh_row0,
-                                                int& sh_rows) {
+/* Tile scheduler (see the file comment): every wave finds this workgroup's
+ * (expert, first row, row count) itself, or expert -1 past the last tile:
+ * the same counts, DPP scan and ballot in each wave, so no LDS broadcast and
+ * barrier stand between the counts and the tile's first loads. The results
+ * are wave-uniform. */
+template <int BM>
+__device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int lane, int& e, int& row0, int& rows) {
     const int per_xcd = gridDim.x / 8;
     const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (wave == 0) {
-        if (a.counts) {
-            const int c = lane < a.n_experts ? min(a.counts[lane * a.count_stride], a.cap) : 0;
-            const int nt = (c + BM - 1) / BM;
-            const int incl = wave_incl_scan(nt);
-            const int excl = incl - nt;
-            const bool mine = lane < a.n_experts && L >= excl && L < incl;
-            const unsigned long long bal = __ballot(mine);
-            if (lane == 0 && bal == 0ull) sh_e = -1;
-            if (mine) {
-                sh_e = lane;
-                sh_row0 = (L - excl) * BM;
-                sh_rows = min(BM, c - (L - excl) * BM);
-            }
-        } else if (lane == 0) {
-            const int row0 = L * BM;
-            sh_e = row0 < a.n_tokens ? 0 : -1;
-            sh_row0 = row0;
-            sh_rows = min(BM, a.n_tokens - row0);
+    if (a.counts) {
+        const int c = lane < a.n_experts ? min(a.counts[lane * a.count_stride], a.cap) : 0;
+        const int nt = (c + BM - 1) / BM;
+        const int incl = wave_incl_scan(nt);
+        const int excl = incl - nt;
+        const bool mine = lane < a.n_experts && L >= excl && L < incl;
+        const unsigned long long bal = __ballot(mine); /* one lane at most */
+        if (bal == 0ull) {
+            e = -1;
+            row0 = rows = 0;
+            return;
         }
+        const int o = __builtin_ctzll(bal);
+        const int ex = __builtin_amdgcn_readlane(excl, o), co = __builtin_amdgcn_readlane(c, o);
+        e = o;
+        row0 = (L - ex) * BM;
+        rows = min(BM, co - row0);
+    } else {
+        row0 = L * BM;
+        e = row0 < a.n_tokens ? 0 : -1;
+        rows = min(BM, a.n_tokens - row0);
     }
 }
 
@@ -128,7 +129,6 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     __shared__ __attribute__((aligned(16))) f16 hs[BM * LDS]; /* raw rows (residual)          */
     __shared__ float s_b1[DIM], s_b2[DIM];
     __shared__ int tok[BM];
-    __shared__ int sh_e, sh_row0, sh_rows;
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -136,12 +136,10 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
     const int g = lane >> 4;
 
     /* ---- schedule ------------------------------------------------------ */
-    expert_schedule<DIM, BM, NT>(a, wave, lane, sh_e, sh_row0, sh_rows);
-    __syncthreads();
-    const int e = __builtin_amdgcn_readfirstlane(sh_e);
+    int e, row0, rows;
+    expert_schedule<BM>(a, lane, e, row0, rows);
 
     if (e >= 0) {
-        const int row0 = sh_row0, rows = sh_rows;
         const FragSrc w1(a.w1 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
         const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
         const int loff = lane * 16;
@@ -384,16 +382,14 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
     __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, GELU output, y */
     __shared__ float s_b1[DIM], s_b2[DIM];
     __shared__ int tok[BM];
-    __shared__ int sh_e, sh_row0, sh_rows;
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
 
-    expert_schedule<DIM, BM, NT>(a, wave, lane, sh_e, sh_row0, sh_rows);
-    __syncthreads();
-    const int e = __builtin_amdgcn_readfirstlane(sh_e);
+    int e, row0, rows;
+    expert_schedule<BM>(a, lane, e, row0, rows);
     if (e < 0) return;
 
     const FragSrc w1(a.w1 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
@@ -404,7 +400,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
         const int q = p % (RT * KS), ks = q / RT, r = q % RT;
         return (p < RT * KS ? w1 : w2).load((wave * RT + r) * KS + ks, loff);
     };
-    expert_stage_tile<DIM, BM, NT>(a, e, sh_row0, sh_rows, s_b1, s_b2, tok);
+    expert_stage_tile<DIM, BM, NT>(a, e, row0, rows, s_b1, s_b2, tok);
     __syncthreads();
 
     /* rows first, then the ring's first fragments; LN2 runs while they arrive */
