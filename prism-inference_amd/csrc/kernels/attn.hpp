@@ -113,18 +113,17 @@ struct AttnLds {
  * those slots' keys and values need the unfolded bias (a separate
  * instantiation keeps that code, and its branches, out of every other
  * window's instruction schedule). vmask bit s: slot s holds a token.
- * HALF (not with PAD): slots 32-63 are all padded (the bottom windows of a
- * grid whose height leaves 4 or fewer rows in the last window row, e.g. 68
- * rows), so token tiles 2 and 3 are never queries, never stored and never
- * routed: only their keys and values are used, and those are the bias alone
- * (the zero LN1 output adds nothing to the accumulator that starts at the
- * bias). The body then computes Q, the softmax rows, O, the out-projection,
- * LN1 and the routing for tiles 0 and 1 only; every stored value is
- * computed as in the full body. */
+ * HALF: slots 32-63 are all padded (the bottom windows of a grid whose
+ * height leaves 4 or fewer rows in the last window row, e.g. 68 rows), so
+ * token tiles 2 and 3 are never queries, never stored and never routed: only
+ * their keys and values are used, and those are the bias alone (the zero LN1
+ * output adds nothing to the accumulator that starts at the bias; with PAD,
+ * the fix-up below sets them). The body then computes Q, the softmax rows,
+ * O, the out-projection, LN1 and the routing for tiles 0 and 1 only; every
+ * stored value is computed as in the full body. */
 template <int DIM, int HD, int NW, int NPT, bool PAD, bool HALF = false>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM, NPT>& L,
                                                  unsigned long long vmask) {
-    static_assert(!(PAD && HALF), "HALF windows take the unpadded body");
     constexpr int TQ = HALF ? 2 : 4; /* token tiles that hold tokens */
     static_assert(DIM / HD == 8, "8 heads");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
@@ -392,7 +391,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
                     /* slots 16t..16t+15 (uniform): all present, all padded
                      * (a bottom-edge window's last rows), or mixed */
                     const unsigned tm = (unsigned)(vmask >> (16 * t)) & 0xffffu;
-                    if (tm == 0u) {
+                    if (t >= TQ || tm == 0u) {
                         k4[c][t] = bk;
                         v4[t][c] = h4{bv, bv, bv, bv};
                     } else if (tm != 0xffffu) {
@@ -632,12 +631,17 @@ __device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>
     const int wy = wi / a.wx, wxx = wi - (wi / a.wx) * a.wx;
     const int lane = lane_id();
     const unsigned long long vmask = __ballot(wy * 8 + (lane >> 3) < a.H && wxx * 8 + (lane & 7) < a.W);
-    if (a.bqkv_pad != nullptr && vmask != ~0ull) /* uniform */
-        attn_window_body<DIM, HD, NW, NPT, true>(a, L, vmask);
-    else if ((vmask >> 32) == 0ull && a.up_w == nullptr)
+    const bool half = (vmask >> 32) == 0ull && a.up_w == nullptr; /* uniform */
+    if (a.bqkv_pad != nullptr && vmask != ~0ull) {
+        if (half)
+            attn_window_body<DIM, HD, NW, NPT, true, true>(a, L, vmask);
+        else
+            attn_window_body<DIM, HD, NW, NPT, true>(a, L, vmask);
+    } else if (half) {
         attn_window_body<DIM, HD, NW, NPT, false, true>(a, L, vmask);
-    else
+    } else {
         attn_window_body<DIM, HD, NW, NPT, false>(a, L, vmask);
+    }
 }
 
 /* 4 waves (2 heads each, 2 workgroups per CU) for large grids; 8 waves (one
