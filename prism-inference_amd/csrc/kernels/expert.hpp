@@ -365,32 +365,42 @@ __device__ __forceinline__ void expert_wide_gemm(f4 (&acc)[RT][TT], h8 (&ring)[P
  * Per output element the arithmetic and its order are those of expert_body
  * (bias in the accumulator, k-steps in order, the same rounding points), so
  * the results are bit-identical to the 64-token kernels.
+ * TA = token tiles computed: an expert's last tile is usually partly empty,
+ * and in the 128-token kernel one with at most 64 rows runs the TA = 4 body,
+ * which gathers, normalises, multiplies, stores and re-reads only those
+ * tiles (the empty tiles' results were never stored).
  */
-template <int DIM, int PF, int BM>
-__device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
+template <int DIM, int BM>
+struct ExpertWideLds {
+    __attribute__((aligned(16))) f16 xs[BM * (DIM + 8)]; /* LN2 output, GELU output, y */
+    float b1[DIM], b2[DIM];
+    int tok[BM];
+};
+
+template <int DIM, int PF, int BM, int TA>
+__device__ __forceinline__ void expert_body_wide(const ExpertArgs& a, ExpertWideLds<DIM, BM>& L, int e, int row0,
+                                                 int rows) {
     constexpr int NW = 4, NT = 64 * NW;
     constexpr int KS = DIM / 32;
     constexpr int LDS = DIM + 8;
-    constexpr int TT = BM / 16;       /* token tiles                   */
     constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave  */
     constexpr int NF = 2 * RT * KS;   /* fragments in the wave's stream */
     constexpr int LPS = DIM / 16;     /* LN lanes per row              */
     constexpr int RPI = 64 / LPS;     /* LN rows per wave iteration    */
     constexpr int IT = BM / NW / RPI;
     static_assert(RT >= 1 && BM % (NW * RPI) == 0 && PF % RT == 0 && PF <= NF, "tile shape");
-
-    __shared__ __attribute__((aligned(16))) f16 xs[BM * LDS]; /* LN2 output, GELU output, y */
-    __shared__ float s_b1[DIM], s_b2[DIM];
-    __shared__ int tok[BM];
+    static_assert(TA >= 2 && TA % 2 == 0 && 16 * TA <= BM, "active tiles (two equal halves)");
+    f16* const xs = L.xs;
+    float* const s_b1 = L.b1;
+    float* const s_b2 = L.b2;
+    int* const tok = L.tok;
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
-
-    int e, row0, rows;
-    expert_schedule<BM>(a, lane, e, row0, rows);
-    if (e < 0) return;
+    /* the waves whose rows all lie past the active tiles skip the row work */
+    const bool rw = wave * (BM / NW) < 16 * TA;
 
     const FragSrc w1(a.w1 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
     const FragSrc w2(a.w2 + (int64_t)e * DIM * DIM, DIM * DIM * 2u);
@@ -406,22 +416,27 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
     /* rows first, then the ring's first fragments; LN2 runs while they arrive */
     RowChunk rc[IT];
     int rt_tok[IT];
+    if (rw) {
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
-        rc[it] = ln_load<DIM>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
+        for (int it = 0; it < IT; ++it) {
+            rt_tok[it] = tok[wave * (BM / NW) + it * RPI + lane / LPS];
+            rc[it] = ln_load<DIM>(a.in, rt_tok[it] >= 0 ? rt_tok[it] : 0); /* none: row 0 */
+        }
     }
     h8 ring[PF];
 #pragma unroll
     for (int p = 0; p < PF; ++p) ring[p] = frag(p);
     sched_fence();
+    if (rw) {
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        const int r = wave * (BM / NW) + it * RPI + lane / LPS;
-        ln_store<DIM, false>(rc[it], rt_tok[it] >= 0, xs + r * LDS, nullptr);
+        for (int it = 0; it < IT; ++it) {
+            const int r = wave * (BM / NW) + it * RPI + lane / LPS;
+            ln_store<DIM, false>(rc[it], rt_tok[it] >= 0, xs + r * LDS, nullptr);
+        }
     }
     __syncthreads();
 
+    constexpr int TT = TA; /* token tiles computed */
     f4 acc[RT][TT];
     h4 res[RT][TT];
     /* ---- GEMM1 + GELU ------------------------------------------------- */
@@ -461,10 +476,12 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
     static_assert(64 % CPR == 0 && (BM / NW) % RPS == 0, "row shape");
     const int c8 = (lane % CPR) * 8;
     h8 hx[NI];
+    if (rw) {
 #pragma unroll
-    for (int it = 0; it < NI; ++it) {
-        const int tk = tok[wave * (BM / NW) + it * RPS + lane / CPR];
-        hx[it] = ld_row16(a.in, ((uint32_t)(tk >= 0 ? tk : 0) * DIM + c8) * 2u); /* none: row 0, unused */
+        for (int it = 0; it < NI; ++it) {
+            const int tk = tok[wave * (BM / NW) + it * RPS + lane / CPR];
+            hx[it] = ld_row16(a.in, ((uint32_t)(tk >= 0 ? tk : 0) * DIM + c8) * 2u); /* none: row 0, unused */
+        }
     }
 #pragma unroll
     for (int r = 0; r < RT; ++r)
@@ -478,14 +495,30 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a) {
             *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g) = res[r][t];
     __syncthreads(); /* y tile complete */
     /* ---- out = y + h in fp16 (one rounding), whole rows --------------- */
+    if (rw) {
 #pragma unroll
-    for (int it = 0; it < NI; ++it) {
-        const int r = wave * (BM / NW) + it * RPS + lane / CPR;
-        const int tk = tok[r];
-        if (tk >= 0)
-            st_row16(a.out, ((uint32_t)tk * DIM + c8) * 2u,
-                     add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]));
+        for (int it = 0; it < NI; ++it) {
+            const int r = wave * (BM / NW) + it * RPS + lane / CPR;
+            const int tk = tok[r];
+            if (tk >= 0)
+                st_row16(a.out, ((uint32_t)tk * DIM + c8) * 2u,
+                         add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]));
+        }
     }
+}
+
+/* Schedules the tile, then runs the body with every token tile, or (SHORT)
+ * with 4 of them when the tile's rows fit there. */
+template <int DIM, int PF, int BM, bool SHORT>
+__device__ __forceinline__ void expert_wide(const ExpertArgs& a, ExpertWideLds<DIM, BM>& L) {
+    static_assert(!SHORT || BM > 64, "the short body is 4 token tiles");
+    int e, row0, rows;
+    expert_schedule<BM>(a, lane_id(), e, row0, rows);
+    if (e < 0) return;
+    if (SHORT && rows <= 64) /* uniform */
+        expert_body_wide<DIM, PF, BM, 4>(a, L, e, row0, rows);
+    else
+        expert_body_wide<DIM, PF, BM, BM / 16>(a, L, e, row0, rows);
 }
 
 /* 4 waves (2 workgroups per CU) for large grids; 8 waves (each streaming half
@@ -505,10 +538,12 @@ extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d128_bm64_w8(E
 /* 128-token tiles, 4 waves, 2 workgroups per CU: the large grids of batched
  * launches (no fused down-projection) */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm128(ExpertArgs a) {
-    expert_body_wide<256, 12, 128>(a);
+    __shared__ ExpertWideLds<256, 128> lds;
+    expert_wide<256, 12, 128, true>(a, lds);
 }
 /* 96-token tiles of the same body: a large stage call's tile count then
  * rounds up to whole rounds of the CUs' workgroup slots with less idle tail */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d256_bm96(ExpertArgs a) {
-    expert_body_wide<256, 12, 96>(a);
+    __shared__ ExpertWideLds<256, 96> lds;
+    expert_wide<256, 12, 96, false>(a, lds); /* the short body measured slower here */
 }
