@@ -28,7 +28,8 @@
  *     wave has finished reading xs; then all heads' O^T go to xs.
  *  4. Out-proj C^T = Wo * O^T, bias, fp16 round, + x from os (fp16 round),
  *     written over the lane's residual in os; the finished tile leaves as
- *     whole 512-byte rows at the very end (16 bytes per lane).
+ *     whole 512-byte rows (16 bytes per lane) after the router GEMM (4 waves)
+ *     or at the very end (8 waves).
  *  5. Routed variants (NPT > 0, the block chain's MoE blocks) route that
  *     output tile from os: waves 0-3 each take 16 tokens through
  *     LN2 + router GEMM + argmax (route_token, whose W_r fragments continue
@@ -535,6 +536,26 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         }
     }
     __syncthreads(); /* y tile complete in os */
+    /* ---- 6. y rows out, 16 bytes per lane (a wave store covers whole rows).
+     * Loads and stores retire through one counter (vmcnt), so a load or a
+     * returning atomic issued after them waits for them too. The 4-wave
+     * kernel (large grids) issues them once the router GEMM's loads are all
+     * out, so they drain during the counting sort; the 8-wave kernel (small
+     * grids, where that sort's device atomics are the critical path) last. */
+    auto store_rows = [&]() {
+        constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
+        constexpr int RPS = 64 / CPR; /* rows per wave store    */
+        static_assert(64 % CPR == 0 && SPW % RPS == 0, "row store shape");
+#pragma unroll
+        for (int it = 0; it < SPW / RPS; ++it) {
+            const int sl = wave * SPW + it * RPS + lane / CPR;
+            const int c8 = (lane % CPR) * 8;
+            const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
+            if (gy < a.H && gx < a.W)
+                st_row16<NW == 8>(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u,
+                                  *reinterpret_cast<const h8*>(os + sl * LDS + c8));
+        }
+    };
 
     /* ---- 5. fused routing (moe_router.comp.glsl:24-52 + counting sort) -- */
     if constexpr (NPT > 0) {
@@ -589,6 +610,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
                 r_rank[sl] = (sy < a.H && sx < a.W) ? atomicAdd(&r_hist[e], 1) : 0;
             }
         }
+        if constexpr (NW == 4) store_rows();
         __syncthreads();
         if (threadIdx.x < a.n_experts) {
             const int c = r_hist[threadIdx.x];
@@ -607,22 +629,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         }
     }
 
-    /* ---- 6. y rows out, 16 bytes per lane (a wave store covers whole rows);
-     * last, so no load above waits behind them (vmcnt counts both) */
-    {
-        constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
-        constexpr int RPS = 64 / CPR; /* rows per wave store    */
-        static_assert(64 % CPR == 0 && SPW % RPS == 0, "row store shape");
-#pragma unroll
-        for (int it = 0; it < SPW / RPS; ++it) {
-            const int sl = wave * SPW + it * RPS + lane / CPR;
-            const int c8 = (lane % CPR) * 8;
-            const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
-            if (gy < a.H && gx < a.W)
-                st_row16<NW == 8>(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u,
-                         *reinterpret_cast<const h8*>(os + sl * LDS + c8));
-        }
-    }
+    if constexpr (NPT == 0 || NW == 8) store_rows();
 }
 
 template <int DIM, int HD, int NW, int NPT>
