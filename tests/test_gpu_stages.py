@@ -44,6 +44,11 @@ def tok_ids(n):
     ("std256", 8, 8, 2),        # exactly one window per frame
     ("moe64", 68, 120, 4),      # 540 windows: the 4-wave kernel
     ("dense128", 68, 120, 4),   # 4-wave kernel, 8 heads x 16
+    # bottom window row with 4 valid rows: slots 32-63 all padded, so those
+    # windows take the body that computes token tiles 0-1 only
+    ("moe64", 12, 16, 2),
+    ("moe64", 13, 16, 2),       # 5 valid rows: the full body, token tile 2 mixed
+    ("moe64", 9, 16, 2),        # 1 valid row: token tile 1 padded as well
 ])
 def test_attention_stage(hip, engine, device_arena, name, H, W, batch):
     cfg = P.CONFIGS[name]
