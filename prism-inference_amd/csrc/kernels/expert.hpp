@@ -468,8 +468,10 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a, ExpertWide
         for (int t = 0; t < TT; ++t) acc[r][t] = bb;
     }
     expert_wide_gemm<KS, LDS, RT, TT, PF, RT * KS, NF>(acc, ring, xs, l16, g, frag);
-    /* the residual rows (L2-resident since the gather) are requested now, so
-     * their latency hides behind the y tile's conversion and barriers */
+    /* the residual rows are fetched a second time now (most have left the
+     * XCD's L2 since the gather), so their latency hides behind the y tile's
+     * conversion and barriers (issued before GEMM2's last k-step instead, in
+     * the registers the weight ring frees there, they measured slower) */
     constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
     constexpr int RPS = 64 / CPR; /* rows per wave access   */
     constexpr int NI = BM / NW / RPS;
