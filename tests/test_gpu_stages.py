@@ -438,3 +438,78 @@ def test_stage_calls_reject_bad_pushes(hip, engine, device_arena):
     hip.sync()
     out = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2)
     assert not (out == 0xFFFF).all()
+
+
+def _with_ln_affine(blob, offs, dim, seed):
+    """A copy of `blob` with LN1/LN2 gamma ~ N(1, 0.3) and beta ~ N(0, 0.2) in
+    every block (trained models' LayerNorms; the engine folds them into the
+    next GEMM's weights, and windows with padded slots then take the bodies
+    that restore the unfolded bias for those slots)."""
+    rng = np.random.default_rng(seed)
+    out = blob.copy()
+    for o in offs:
+        for g_off, b_off in ((o.ln1_g, o.ln1_b), (o.ln2_g, o.ln2_b)):
+            out[g_off:g_off + dim] = O.f32_to_f16bits(rng.normal(1.0, 0.3, dim).astype(np.float32))
+            out[b_off:b_off + dim] = O.f32_to_f16bits(rng.normal(0.0, 0.2, dim).astype(np.float32))
+    return out
+
+
+def _random_grid_cases(n, seed=2024):
+    rng = np.random.default_rng(seed)
+    names = ("moe64", "moe16", "moe24d128")
+    cases = []
+    for i in range(n):
+        H, W = int(rng.integers(8, 73)), int(rng.integers(8, 73))
+        cases.append((names[i % 3], H, W, int(rng.integers(1, 4)), bool(i % 2)))
+    cases.append(("moe64", 64, 64, 8, True))    # exactly 512 windows: the 4-wave kernel
+    cases.append(("moe16", 69, 64, 8, False))   # 4-wave, bottom windows with 5 valid rows
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,H,W,batch,affine", _random_grid_cases(8))
+def test_attn_route_random_grids(hip, engine, device_arena, name, H, W, batch, affine):
+    """Seeded random grids (8..72 on each axis, 1-3 frames, with and without
+    LayerNorm affines) through prism_attn_route against the oracle: every
+    window shape the window mapping produces (full, padded rows and/or
+    columns, a bottom window row of 1-4 valid rows whose padded token tiles
+    are skipped), 4- and 8-wave kernels, d256 and d128. Output within the
+    block tolerances, routing exact on every token whose top-1/top-2 gap is
+    >= 1e-2, counts and buckets consistent with the assignments."""
+    cfg = FUSED_EXTRA[name] if name in FUSED_EXTRA else P.CONFIGS[name]
+    desc, blob, offs, _ = make_model(cfg, 1, H, W)
+    if affine:
+        blob = _with_ln_affine(blob, offs, cfg.dim, seed=H * 100 + W)
+    engine.load_weights(desc, blob, offs)
+    w = f16(blob)
+    n, d, N = batch * H * W, cfg.dim, cfg.n_experts
+    windows = batch * ((H + 7) // 8) * ((W + 7) // 8)
+    x = P.synth_features(cfg, batch=batch, H=H, W=W, seed=H + W).reshape(n, d)
+    feats = device_arena(2 * n * d * 2)
+    aux_n = P.aux_elems(N, n)
+    aux = device_arena(aux_n * 4)
+    hip.upload(feats.ptr, x)
+    hip.memset(aux.ptr, 0xFF, aux_n * 4)
+    print(f"[random grid] {name} {H}x{W} batch {batch} affine {affine}: "
+          f"{attn_kernel(cfg.dim, N, windows)}, {windows} windows", flush=True)
+    pa = engine.attn_push(0, 0, n * d, H, W)
+    pr = engine.router_push(0, H * W, n * d, 0, n, n + N)
+    assert engine.attn_route(pa, pr, feats.ptr, aux.ptr, batch) == 0, engine.error()
+    hip.sync()
+    h = f16(hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2)).reshape(n, d)
+    host = hip.download(np.empty(aux_n, np.int32), aux.ptr)
+    assign, counts, perm = host[:n], host[n:n + N], host[n + N:].reshape(N, n)
+    c = ocfg(cfg, H, W, batch)
+    h_ref = O.attn_stage(c, w, offs[0], f16(x))
+    mx, mean = errors(h, h_ref)
+    ref_assign, logits = O.router_stage(c, w, offs[0], h_ref)
+    top2 = np.sort(logits, axis=1)[:, -2:]
+    sure = (top2[:, 1] - top2[:, 0]) >= GAP
+    print(f"[random grid] max {mx:.3g} mean {mean:.3g}, {int((assign != ref_assign).sum())} of {n} experts "
+          f"differ, {int((~sure).sum())} near ties")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+    assert ((assign >= 0) & (assign < N)).all()
+    assert (assign[sure] == ref_assign[sure]).all()
+    assert (counts == np.bincount(assign, minlength=N)).all()
+    for e in range(N):
+        assert (np.sort(perm[e, :counts[e]]) == np.nonzero(assign == e)[0]).all(), f"bucket {e}"
