@@ -513,3 +513,45 @@ def test_attn_route_random_grids(hip, engine, device_arena, name, H, W, batch, a
     assert (counts == np.bincount(assign, minlength=N)).all()
     for e in range(N):
         assert (np.sort(perm[e, :counts[e]]) == np.nonzero(assign == e)[0]).all(), f"bucket {e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,H,W,batch", [
+    ("moe64", 23, 51, 1),        # small grid: 8-wave 64-token tiles
+    ("moe16", 48, 72, 10),       # 34,560 tokens: 4-wave 64-token tiles
+    ("moe64", 68, 120, 8),       # 65,280 tokens: 96-token tiles (stage call of the wide size)
+    ("moe32", 70, 90, 11),       # 69,300 tokens, ragged grid, 96-token tiles
+    ("moe24d128", 40, 40, 5),    # d128
+])
+def test_experts_random_loads(hip, engine, device_arena, name, H, W, batch):
+    """The router + expert stage calls on grids whose expert segments end in
+    partial tiles of every length, through each expert kernel a stage call
+    can choose; the outputs of a sample of tokens (all of the three least
+    loaded experts, whose tiles are the most partial, plus 3,000 at random)
+    against the oracle, teacher-forced with the GPU's routing."""
+    cfg = FUSED_EXTRA[name] if name in FUSED_EXTRA else P.CONFIGS[name]
+    desc, blob, offs, w = make_model(cfg, 1, H, W)
+    engine.load_weights(desc, blob, offs)
+    T, d, N = H * W, cfg.dim, cfg.n_experts
+    n = batch * T
+    h_bits = P.synth_features(cfg, batch=batch, H=H, W=W, seed=3 * H + W).reshape(n, d)
+    feats = device_arena(2 * n * d * 2)
+    hip.upload(feats.ptr, h_bits)
+    aux = device_arena(P.aux_elems(N, n) * 4)
+    print(f"[expert loads] {name} {H}x{W} batch {batch}", flush=True)
+    assert engine.router(engine.router_push(0, T, 0, 0, n, n + N), feats.ptr, aux.ptr, batch) == 0, engine.error()
+    assert engine.experts(engine.expert_push(0, T, 0, n * d, 0, n, n + N), feats.ptr, aux.ptr, batch) == 0, \
+        engine.error()
+    hip.sync()
+    y = hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2).reshape(n, d)
+    assign = hip.download(np.empty(n, np.int32), aux.ptr)
+    counts = np.bincount(assign, minlength=N)
+    cold = np.argsort(counts)[:3]
+    rng = np.random.default_rng(H * W)
+    idx = np.unique(np.concatenate([np.nonzero(np.isin(assign, cold))[0],
+                                    rng.choice(n, min(n, 3000), replace=False)]))
+    ref = O.expert_stage(ocfg(cfg, 1, len(idx), 1), w, offs[0], f16(h_bits[idx]), assign[idx])
+    mx, mean = errors(f16(y[idx]), ref)
+    print(f"[expert loads] {len(idx)} sampled tokens, max {mx:.3g} mean {mean:.3g}; tail rows of each expert's "
+          f"last 64-token tile: {sorted(set((counts % 64).tolist()))[:8]}...")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
