@@ -120,8 +120,9 @@ struct AttnLds {
  * their keys and values are used, and those are the bias alone (the zero LN1
  * output adds nothing to the accumulator that starts at the bias; with PAD,
  * the fix-up below sets them). The body then computes Q, the softmax rows,
- * O, the out-projection, LN1 and the routing for tiles 0 and 1 only; every
- * stored value is computed as in the full body. */
+ * O, the out-projection, LN1 (and the fused up-projection) and the routing
+ * for tiles 0 and 1 only; every stored value is computed as in the full
+ * body. */
 template <int DIM, int HD, int NW, int NPT, bool PAD, bool HALF = false>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM, NPT>& L,
                                                  unsigned long long vmask) {
@@ -278,13 +279,13 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
 #pragma unroll
         for (int ks = 0; ks < UKS; ++ks)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < TQ; ++t) {
                 const h8 xf = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * ks + 8 * g);
 #pragma unroll
                 for (int r = 0; r < UPR; ++r) uacc[r][t] = mfma_16x16x32(wup[r][ks], xf, uacc[r][t]);
             }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TQ; ++t) {
             const int sl = 16 * t + l16;
             const bool ok = wy * 8 + (sl >> 3) < a.H && wxx * 8 + (sl & 7) < a.W;
 #pragma unroll
@@ -298,13 +299,15 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             }
         }
         __syncthreads(); /* x complete in os; the staging in xs is dead */
+        if (lnw) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
-            const int ca = (lane % LPS) * 8;
-            const RowChunk xr{*reinterpret_cast<const h8*>(os + row + ca),
-                              *reinterpret_cast<const h8*>(os + row + ca + DIM / 2)};
-            ln_store<DIM>(xr, valid[it], xs + row, nullptr);
+            for (int it = 0; it < IT; ++it) {
+                const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+                const int ca = (lane % LPS) * 8;
+                const RowChunk xr{*reinterpret_cast<const h8*>(os + row + ca),
+                                  *reinterpret_cast<const h8*>(os + row + ca + DIM / 2)};
+                ln_store<DIM>(xr, valid[it], xs + row, nullptr);
+            }
         }
     }
     __syncthreads();
@@ -638,7 +641,7 @@ __device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>
     const int wy = wi / a.wx, wxx = wi - (wi / a.wx) * a.wx;
     const int lane = lane_id();
     const unsigned long long vmask = __ballot(wy * 8 + (lane >> 3) < a.H && wxx * 8 + (lane & 7) < a.W);
-    const bool half = (vmask >> 32) == 0ull && a.up_w == nullptr; /* uniform */
+    const bool half = (vmask >> 32) == 0ull; /* uniform */
     if (a.bqkv_pad != nullptr && vmask != ~0ull) {
         if (half)
             attn_window_body<DIM, HD, NW, NPT, true, true>(a, L, vmask);
