@@ -251,8 +251,9 @@ def main():
     # ---- batch-B throughput (the step) and batch-1 latency, hipGraph replay
     log(f"[bench] batch {B}: warmup {args.warmup}, steps {args.steps}")
     ms_b, wall_b = time_graph(hip, eng, dx, dy, B, args.steps, args.warmup, stream)
-    assign_ptr, ntok = eng.forward_assignments()
-    assign = hip.download(np.empty(cfg.n_blocks * ntok, np.int32), assign_ptr).reshape(cfg.n_blocks, ntok)
+    if cfg.n_experts > 1:
+        assign_ptr, ntok = eng.forward_assignments()
+        assign = hip.download(np.empty(cfg.n_blocks * ntok, np.int32), assign_ptr).reshape(cfg.n_blocks, ntok)
     log(f"[bench] batch 1 latency")
     ms_1, _ = time_graph(hip, eng, dx, dy, 1, max(args.steps, 50), args.warmup, stream)
 
@@ -269,23 +270,33 @@ def main():
     aux_n = P.aux_elems(N, n)
     aux = hip.malloc(aux_n * 4)
     hip.memset(aux, 0, aux_n * 4)
+    moe = N > 1
     a_push = eng.attn_push(0, 0, n * d)
-    r_push = eng.router_push(0, T, n * d, 0, n, n + N)
-    e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N)
     log("[bench] per-stage timing")
     t_attn = time_stage(hip, lambda: eng.attn(a_push, feats, B, stream), args.stage_reps, stream)
-    # the chain's MoE-block kernel: attention + routing in one launch (plus the
-    # one-workgroup counter clear the stage call issues before it)
-    rr_push = eng.router_push(0, T, n * d, 0, n, n + N)
-    t_route = time_stage(hip, lambda: eng.attn_route(a_push, rr_push, feats, aux, B, stream), args.stage_reps,
-                         stream)
-    # the router launch clears its counts itself; the expert stage only reads them
-    t_router = time_stage(hip, lambda: eng.router(r_push, feats, aux, B, stream), args.stage_reps, stream)
-    t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, aux, B, stream), args.stage_reps, stream)
+    attn_grid = ((cfg.W + 7) // 8) * ((cfg.H + 7) // 8) * B
+    kname = f"prism_attn_d{d}" + ("_w8" if attn_grid < 512 else "")
+    if moe:
+        r_push = eng.router_push(0, T, n * d, 0, n, n + N)
+        e_push = eng.expert_push(0, T, n * d, 0, 0, n, n + N)
+        # the chain's MoE-block kernel: attention + routing in one launch (plus
+        # the one-workgroup counter clear the stage call issues before it)
+        rr_push = eng.router_push(0, T, n * d, 0, n, n + N)
+        t_route = time_stage(hip, lambda: eng.attn_route(a_push, rr_push, feats, aux, B, stream), args.stage_reps,
+                             stream)
+        # the router launch clears its counts itself; the expert stage only reads them
+        t_router = time_stage(hip, lambda: eng.router(r_push, feats, aux, B, stream), args.stage_reps, stream)
+        t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, aux, B, stream), args.stage_reps, stream)
+        kname += f"_r{(N + 15) // 16}"
+        timed = "prism_attn_route stage call: the routed attention kernel + its 1-workgroup count copy"
+    else:
+        # dense blocks: attention, then the FFN as the expert stage with one expert
+        e_push = eng.expert_push(0, T, n * d, 0)
+        t_route, t_router = t_attn, None
+        t_expert = time_stage(hip, lambda: eng.experts(e_push, feats, None, B, stream), args.stage_reps, stream)
+        timed = "prism_attn stage call: the attention kernel"
     route_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * n
     route_tflops = route_flops / (t_route * 1e-3) / 1e12
-    attn_grid = ((cfg.W + 7) // 8) * ((cfg.H + 7) // 8) * B
-    kname = "prism_attn_d256_r4"
     traffic, traffic_src = measured_traffic(kname, attn_grid) if cfg.name == "moe64" else (None, None)
 
     # ---- projection adapters: the stage launches at batch B, and the adapted
@@ -314,12 +325,23 @@ def main():
                         "expert launch"}
     for ptr in (proj, ax, ay):
         hip.free(ptr)
-    log("[bench] end-to-end frame and codec stages")
-    e2e = codec_section(hip, eng, desc, max(20, args.steps // 2), 5, args.stage_reps, stream)
+    # the reference's end-to-end frame renders at 960x540, which encodes to the 68x120 grid
+    e2e = None
+    if P.codec_resolutions()[-1] == (cfg.W, cfg.H):
+        log("[bench] end-to-end frame and codec stages")
+        e2e = codec_section(hip, eng, desc, max(20, args.steps // 2), 5, args.stage_reps, stream)
 
     # ---- expert load actually produced (all blocks, batch B)
-    share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
-    hist0 = np.bincount(assign[0], minlength=N)
+    expert_load = None
+    if moe:
+        share = np.array([np.bincount(a, minlength=N).max() / a.size for a in assign])
+        hist0 = np.bincount(assign[0], minlength=N)
+        expert_load = {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
+                       "hottest_share_mean": round(float(share.mean()), 4),
+                       "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)}
+    routing = {P.ROUTE_RANDOM: "N(0,0.02) router bias", P.ROUTE_UNIFORM: "uniform-load router bias",
+               P.ROUTE_ZIPF: "Zipf(1.1)-fitted router bias",
+               P.ROUTE_ADVERSARIAL: "adversarial router bias (half the tokens to one expert)"}[cfg.routing]
 
     out = {
         "metric": METRIC,
@@ -333,9 +355,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, Zipf(1.1)-fitted router bias)",
-        "config": {"workload": f"{cfg.name}: d{d} x {cfg.n_blocks} blocks, 8x32 heads, 8x8 windows, "
-                               f"{N} experts top-1, {cfg.H}x{cfg.W} tokens, batch {B}",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights"
+                + (f", {routing})" if moe else ")"),
+        "config": {"workload": f"{cfg.name}: d{d} x {cfg.n_blocks} blocks, {cfg.n_heads}x{cfg.head_dim} heads, "
+                               f"8x8 windows, " + (f"{N} experts top-1, " if moe else "dense FFN, ")
+                               + f"{cfg.H}x{cfg.W} tokens, batch {B}",
                    "batch": B, "tokens_per_frame": T, "blocks": cfg.n_blocks, "experts": N,
                    "parallelism": "single GPU"},
         "us_per_frame": round(ms_b * 1e3 / B, 3),
@@ -343,18 +367,17 @@ def main():
         "batch1": {"frames_per_s": round(1e3 / ms_1, 2), "us_per_frame": round(ms_1 * 1e3, 2),
                    "mfma_frac": round(flops_frame / (ms_1 * 1e-3) / MFMA_F16_PEAK, 4),
                    "hbm_frac": round((weight_bytes + io_bytes_1) / (ms_1 * 1e-3) / HBM_PEAK, 4)},
-        "stages_ms": {"attention_routed": round(t_route, 5), "experts": round(t_expert, 5),
-                      "attention_stage": round(t_attn, 5), "router_stage": round(t_router, 5), "batch": B},
+        "stages_ms": {"attention_routed": round(t_route, 5) if moe else None, "experts": round(t_expert, 5),
+                      "attention_stage": round(t_attn, 5),
+                      "router_stage": round(t_router, 5) if moe else None, "batch": B},
         "roofline": {"kernel": kname, "bound": "mfma", "achieved": round(route_tflops, 2),
                      "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": round(route_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "traffic_source": traffic_src,
                      "flops_per_launch": route_flops, "avg_launch_ms": round(t_route, 5),
-                     "timed": "prism_attn_route stage call: the routed attention kernel + its 1-workgroup count copy"},
-        "expert_load": {"hottest_share_block0": round(float(hist0.max() / hist0.sum()), 4),
-                        "hottest_share_mean": round(float(share.mean()), 4),
-                        "coldest_share_block0": round(float(hist0.min() / hist0.sum()), 5)},
+                     "timed": timed},
+        "expert_load": expert_load,
         "wall_s_timed": round(wall_b, 3),
         "adapters": adapters,
         "e2e_frame": e2e,
