@@ -239,10 +239,11 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
      * block's expert stage of the previous chain, has finished) */
     if (NPT > 0 && a.zero_next && blockIdx.x == 0 && threadIdx.x < a.n_experts)
         a.zero_next[threadIdx.x * a.count_stride] = 0;
-    /* every parameter is staged now: a load issued after the residual
-     * prefetch below would make its LDS store wait for that HBM fetch. The
-     * barrier after LN1 publishes them (each wave starts its LN1 as soon as
-     * its own rows are in, without waiting for the other waves' stores) */
+    /* every parameter is staged here, before LN1: loads retire in issue
+     * order, so these LDS stores wait only for the rows and the ring's first
+     * fragments, which LN1 and the QKV GEMM wait for anyway. The barrier
+     * after LN1 publishes them (each wave starts its LN1 as soon as its own
+     * rows are in, without waiting for the other waves' stores) */
     for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
     if constexpr (PAD)
         for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv_pad[i] = a.bqkv_pad[i];
