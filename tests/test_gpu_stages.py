@@ -249,6 +249,7 @@ def attn_kernel(dim, n_experts, windows):
 @pytest.mark.parametrize("name,H,W,batch,kernel", [
     ("moe64", 68, 120, 1, "prism_attn_d256_w8_r4"),
     ("moe64", 68, 120, 4, "prism_attn_d256_r4"),       # 540 windows
+    ("moe64", 68, 120, 16, "prism_attn_d256_r4"),      # the headline batch: 2,160 windows
     ("moe16", 9, 13, 1, "prism_attn_d256_w8_r1"),      # one row tile, ragged windows
     ("moe40", 68, 120, 1, "prism_attn_d256_w8_r3"),    # 3 row tiles, 24 padded experts
     ("moe24d128", 68, 120, 2, "prism_attn_d128_w8_r2"),
