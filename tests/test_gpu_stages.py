@@ -97,6 +97,7 @@ def _router_case(hip, engine, device_arena, name, H, W, batch):
     ("moe16", 68, 120, 2),
     ("moe32", 135, 240, 1),
     ("moe64", 9, 13, 1),
+    ("moe64", 68, 120, 16),      # the headline batch: 96-token expert tiles, 1,424 workgroups
 ])
 def test_router_then_experts(hip, engine, device_arena, name, H, W, batch):
     cfg, c, w, offs, n, d, N, h, feats, aux, host, (a_off, c_off, p_off) = _router_case(
