@@ -141,6 +141,32 @@ def codec_section(hip, eng, desc, steps, warmup, reps, stream):
                         "hipGraph replay; codec weights ~N(0, 2/K)"}
 
 
+def chain_launches(eng, dx, dy, batch, stream, reps=5):
+    """The chain's own attention and expert launches, run one after another
+    (prism_chain_launch_times: the kernels, grids and arguments of
+    prism_forward, HIP events between launches on the launch stream): median
+    over `reps` chains of the mean launch durations (ms), and the grids."""
+    a, e = [], []
+    ga = ge = 0
+    for _ in range(reps):
+        ta, te, ga, ge = eng.chain_launch_times(dx, dy, batch, stream)
+        a.append(ta)
+        e.append(te)
+    return statistics.median(a), statistics.median(e), ga, ge
+
+
+def expert_kernel(d, tokens, n_experts):
+    """The expert kernel the engine's chain launches for `tokens` tokens: 128-
+    token tiles for d256 grids of >= 512 of them, else 64-token tiles (8 waves
+    below 512); grids hold ceil(tokens / tile) + one partial tile per expert,
+    rounded up to 8."""
+    part = n_experts if n_experts > 1 else 0
+    tiles = lambda bm: ((tokens + bm - 1) // bm + part + 7) // 8 * 8
+    if d == 256 and tiles(128) >= 512:
+        return f"prism_expert_d{d}_bm128"
+    return f"prism_expert_d{d}_bm64" + ("_w8" if tiles(64) < 512 else "")
+
+
 def measured_traffic(kernel, grid):
     """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (calibrated against a device copy of known size), if it covers this
@@ -213,6 +239,51 @@ def cpu_baseline(cfg, blob, offs, x_bits, budget_s, batch):
     return out
 
 
+# The other workloads of the path, each at its stated batch and at batch 1
+# (the headline MoE-64 line is the main measurement).
+OTHER_CONFIGS = [("dense128", 16), ("std256", 16), ("moe16", 16), ("moe32", 4)]
+
+
+def config_section(hip, name, batch, steps, stream):
+    """ms per graph step at `batch` and at batch 1, and the chain's attention
+    launch against the MFMA roofline, for one of the other workloads."""
+    cfg = P.CONFIGS[name]
+    desc = cfg.desc()
+    blob, offs = P.synth_weights(desc, seed=0, routing=cfg.routing)
+    eng = P.Engine(0)
+    try:
+        eng.load_weights(desc, blob, offs)
+        T, d = cfg.tokens, cfg.dim
+        dx, dy = hip.malloc(batch * T * d * 2), hip.malloc(batch * T * d * 2)
+        try:
+            hip.upload(dx, P.synth_features(cfg, batch=batch, seed=1))
+            ms_b, _ = time_graph(hip, eng, dx, dy, batch, steps, 3, stream)
+            ms_1, _ = time_graph(hip, eng, dx, dy, 1, steps, 3, stream)
+            ta, te, ga, ge = chain_launches(eng, dx, dy, batch, stream, reps=3)
+        finally:
+            hip.free(dx)
+            hip.free(dy)
+    finally:
+        eng.close()
+    flops_frame = cfg.flops_per_token_block() * T * cfg.n_blocks
+    S = max(1, min(2, batch // 2))  # the engine's sub-chains (CHAIN_SPLIT = 2 of >= 2 frames)
+    tok_launch = batch * T // S
+    a_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * tok_launch
+    e_flops = 2 * 2 * d * d * tok_launch
+    kern = f"prism_attn_d{d}" + ("_w8" if ga < 512 else "") + (f"_r{(cfg.n_experts + 15) // 16}" if cfg.n_experts > 1 else "")
+    return {"batch": batch, "ms_per_step": round(ms_b, 5), "frames_per_s": round(batch / (ms_b * 1e-3), 2),
+            "mfma_frac": round(flops_frame * batch / (ms_b * 1e-3) / MFMA_F16_PEAK, 4),
+            "batch1_us_per_frame": round(ms_1 * 1e3, 2),
+            "batch1_mfma_frac": round(flops_frame / (ms_1 * 1e-3) / MFMA_F16_PEAK, 4),
+            "roofline": {"kernel": kern, "grid": ga, "avg_launch_ms": round(ta, 5),
+                         "frac": round(a_flops / (ta * 1e-3) / MFMA_F16_PEAK, 4),
+                         "expert_grid": ge, "expert_avg_launch_ms": round(te, 5),
+                         "expert_frac": round(e_flops / (te * 1e-3) / MFMA_F16_PEAK, 4)},
+            "workload": f"d{d} x {cfg.n_blocks} blocks, {cfg.n_heads}x{cfg.head_dim} heads, "
+                        + (f"{cfg.n_experts} experts top-1, " if cfg.n_experts > 1 else "dense FFN, ")
+                        + f"{cfg.H}x{cfg.W} tokens"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -223,6 +294,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stage-reps", type=int, default=20)
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workloads' section")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -299,6 +371,20 @@ def main():
     route_tflops = route_flops / (t_route * 1e-3) / 1e12
     traffic, traffic_src = measured_traffic(kname, attn_grid) if cfg.name == "moe64" else (None, None)
 
+    # ---- the step's own launches: the chain's attention and expert kernels at
+    # the grids the graph replays (batch 16: two sub-chains of 8 frames), run
+    # one after another with HIP events between them
+    log("[bench] chain launches")
+    c_attn, c_exp, c_ga, c_ge = chain_launches(eng, dx, dy, B, stream)
+    S = max(1, min(2, B // 2))  # sub-chains of the engine (CHAIN_SPLIT = 2 of >= 2 frames)
+    tok_launch = n // S
+    c_attn_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * tok_launch
+    c_exp_flops = 2 * 2 * d * d * tok_launch
+    c_kname = f"prism_attn_d{d}" + ("_w8" if c_ga < 512 else "") + (f"_r{(N + 15) // 16}" if moe else "")
+    c_ename = expert_kernel(d, tok_launch, N)
+    c_traffic, c_traffic_src = measured_traffic(c_kname, c_ga) if cfg.name == "moe64" else (None, None)
+    c_etraffic, _ = measured_traffic(c_ename, c_ge) if cfg.name == "moe64" else (None, None)
+
     # ---- projection adapters: the stage launches at batch B, and the adapted
     # chain (up -> blocks -> down, the projections fused into the first and
     # last launches) as one graph step
@@ -370,13 +456,36 @@ def main():
         "stages_ms": {"attention_routed": round(t_route, 5) if moe else None, "experts": round(t_expert, 5),
                       "attention_stage": round(t_attn, 5),
                       "router_stage": round(t_router, 5) if moe else None, "batch": B},
-        "roofline": {"kernel": kname, "bound": "mfma", "achieved": round(route_tflops, 2),
+        "roofline": {"kernel": c_kname, "grid": c_ga, "bound": "mfma",
+                     "achieved": round(c_attn_flops / (c_attn * 1e-3) / 1e12, 2),
                      "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": round(route_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
+                     "frac": round(c_attn_flops / (c_attn * 1e-3) / MFMA_F16_PEAK, 4), "traffic": c_traffic,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-                     "traffic_source": traffic_src,
-                     "flops_per_launch": route_flops, "avg_launch_ms": round(t_route, 5),
-                     "timed": timed},
+                     "traffic_source": c_traffic_src,
+                     "flops_per_launch": c_attn_flops, "avg_launch_ms": round(c_attn, 5),
+                     "timed": f"the batch-{B} chain's own attention launches ({c_ga} workgroups, {tok_launch} tokens "
+                              "each), run one after another by prism_chain_launch_times: HIP events between "
+                              "launches on the launch stream, median over 5 chains of the mean over the chain's "
+                              f"{cfg.n_blocks * S} launches",
+                     "chain_launches": {
+                         "attention": {"kernel": c_kname, "grid": c_ga, "flops": c_attn_flops,
+                                       "avg_launch_ms": round(c_attn, 5),
+                                       "frac": round(c_attn_flops / (c_attn * 1e-3) / MFMA_F16_PEAK, 4),
+                                       "traffic": c_traffic},
+                         "experts": {"kernel": c_ename, "grid": c_ge, "flops": c_exp_flops,
+                                     "avg_launch_ms": round(c_exp, 5),
+                                     "frac": round(c_exp_flops / (c_exp * 1e-3) / MFMA_F16_PEAK, 4),
+                                     "traffic": c_etraffic},
+                         "both": {"flops": c_attn_flops + c_exp_flops, "ms": round(c_attn + c_exp, 5),
+                                  "frac": round((c_attn_flops + c_exp_flops) / ((c_attn + c_exp) * 1e-3)
+                                                / MFMA_F16_PEAK, 4),
+                                  "note": "one block of one sub-chain, its two launches alone on the GPU; the "
+                                          "graph overlaps one sub-chain's expert launch with the other's "
+                                          "attention launch"}},
+                     "stage_call": {"kernel": kname, "grid": attn_grid, "flops": route_flops,
+                                    "avg_launch_ms": round(t_route, 5),
+                                    "frac": round(route_tflops * 1e12 / MFMA_F16_PEAK, 4), "traffic": traffic,
+                                    "timed": timed}},
         "expert_load": expert_load,
         "wall_s_timed": round(wall_b, 3),
         "adapters": adapters,
@@ -384,6 +493,12 @@ def main():
     }
     hip.free(feats)
     hip.free(aux)
+
+    if cfg.name == "moe64" and not args.no_configs:
+        out["configs"] = {}
+        for name, b in OTHER_CONFIGS:
+            log(f"[bench] config {name} batch {b}")
+            out["configs"][name] = config_section(hip, name, b, 10, stream)
 
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle)")

@@ -235,9 +235,25 @@ int prism_forward_graph(prism_ctx* ctx, const void* in, void* out, int32_t batch
  * (2*n*dim*2 + n_blocks*n*4 + n_experts*n*4 bytes + the counter rows, n =
  * batch*H*W; e.g. MoE-64 d256 x 16 blocks at 68x120 fits at batch 1) is
  * refused with PRISM_ERR_INVALID before any launch. The array keeps the last
- * call's contents (the call clears the counters it needs first); calls on one
- * GPU that overlap in time, from any context, share the array and race. */
+ * call's contents (the call clears the counters it needs first). Calls on one
+ * GPU, from any context, stream or host thread, share the array and run one
+ * after another: each call's stream first waits for the previous call's
+ * launches (one event per GPU, recorded after every call). Under stream
+ * capture that wait is not recorded into the graph, so replays of a captured
+ * call are ordered only by the stream the caller launches them on. */
 int prism_forward_noalloc(prism_ctx* ctx, const void* in, void* out, int32_t batch, void* stream);
+
+/* Measurement aid, no counterpart in the reference (the reference times its
+ * recorded frame with timestamp queries around the whole chain,
+ * prism_moe_bench.cpp:183-209). Runs the launches of prism_forward for
+ * `batch` frames (the same kernels, grids and arguments, sub-chain by
+ * sub-chain) one after another on `stream`, with an event between every two
+ * launches, waits for them, and returns the mean duration in ms of the
+ * chain's attention launches (attn_ms) and of its expert launches
+ * (expert_ms), and the workgroup count of each (the first launch of each
+ * kind). `out` receives the chain's output, as from prism_forward. */
+int prism_chain_launch_times(prism_ctx* ctx, const void* in, void* out, int32_t batch, void* stream,
+                             float* attn_ms, float* expert_ms, int32_t* attn_grid, int32_t* expert_grid);
 
 /* Device pointer to the expert assignment of every block of the most recent
  * forward: [n_blocks][batch*H*W] int32. */

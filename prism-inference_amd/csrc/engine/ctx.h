@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -109,6 +110,7 @@ struct prism_ctx {
     const int32_t* fwd_assign = nullptr; /* [n_blocks][fwd_tokens] of the last forward */
     void* scratch = nullptr;      /* this device's allocation-free workspace (scratch.hip) */
     bool counts_dirty = false;    /* block 0's counters may be nonzero */
+    unsigned last_grid = 0;       /* workgroups of the last kernel launched (chain timing) */
     int32_t* stage_counts = nullptr; /* prism_attn_route: private counters, CHAIN_COUNT_STRIDE apart */
     bool stage_dirty = false;        /* ... possibly nonzero (a call stopped between its launches) */
 
@@ -146,8 +148,14 @@ static constexpr size_t PRISM_SCRATCH_BYTES = size_t(16) << 20;
 static constexpr int PRISM_SCRATCH_MAX_DEVICES = 64;
 
 /* scratch.hip: the scratch array's address on `device` (which must be the
- * current device), taken once per device and kept. */
+ * current device), taken once per device and kept, together with the
+ * device's completion event for the array's calls. */
 hipError_t scratch_device_address(int device, void** out);
+/* the event the last prism_forward_noalloc on `device` recorded after its
+ * launches (created by scratch_device_address), and the host lock that
+ * orders those calls */
+hipEvent_t scratch_done_event(int device);
+std::mutex& scratch_call_mutex(int device);
 
 /* Record the message on the context (if any) and the thread; returns code. */
 int fail(prism_ctx* c, int code, const char* fmt, ...);

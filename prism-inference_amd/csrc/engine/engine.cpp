@@ -307,6 +307,9 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
 
     (void)hipDeviceSynchronize();
     drop_graph(c);
+    /* the last forward's assignments belong to the weights being replaced */
+    c->fwd_assign = nullptr;
+    c->fwd_tokens = 0;
     if (c->warena) {
         (void)hipFree(c->warena);
         c->warena = nullptr;
@@ -455,6 +458,7 @@ int launch(prism_ctx* c, hipFunction_t f, unsigned grid, A& args, hipStream_t s,
     void* params[] = {&args};
     hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+    c->last_grid = grid;
     return PRISM_OK;
 }
 
@@ -860,8 +864,30 @@ static int ensure_workspace(prism_ctx* c, int batch, bool io = false) {
  * attention runs the up-projection in its prologue and the last block's
  * expert stage the down-projection in its epilogue, the blocks in between
  * ping-pong through the 256-channel buffers (ws.io, ws.scratch). */
+/* Events between the launches of a timed chain (prism_chain_launch_times):
+ * ev[0] before the first launch, ev[i] after launch i, whose kind (0 =
+ * attention, 1 = experts) and grid are kept. */
+struct ChainTimer {
+    std::vector<hipEvent_t> ev;
+    std::vector<int> kind;
+    std::vector<unsigned> grid;
+    size_t n = 0; /* events recorded */
+};
+
+static int timer_mark(prism_ctx* c, ChainTimer* tm, int kind, hipStream_t s) {
+    if (!tm) return PRISM_OK;
+    if (tm->n >= tm->ev.size()) return fail(c, PRISM_ERR_STATE, "chain timer: more launches than events");
+    HIP_TRY(c, hipEventRecord(tm->ev[tm->n], s));
+    if (tm->n > 0) {
+        tm->kind.push_back(kind);
+        tm->grid.push_back(c->last_grid);
+    }
+    ++tm->n;
+    return PRISM_OK;
+}
+
 static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int nf, const uint16_t* in,
-                            uint16_t* out, hipStream_t s, bool adapted = false) {
+                            uint16_t* out, hipStream_t s, bool adapted = false, ChainTimer* tm = nullptr) {
     const int NB = c->desc.n_blocks, H = c->desc.spatial_h, W = c->desc.spatial_w, D = c->desc.dim;
     const int N = c->desc.n_experts;
     const bool moe = N > 1;
@@ -886,13 +912,15 @@ static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int 
             const RouteOut ro{ws.assign + (size_t)b * n_all + t0, counts, perm, CHAIN_COUNT_STRIDE,
                               NB > 1 ? counts0 + (size_t)((b + 1) % NB) * row : nullptr};
             int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro, first);
-            if (rc) return rc;
-            rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last);
+            if (!rc) rc = timer_mark(c, tm, 0, s);
+            if (!rc) rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last);
+            if (!rc) rc = timer_mark(c, tm, 1, s);
             if (rc) return rc;
         } else {
             int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, nullptr, first);
-            if (rc) return rc;
-            rc = enqueue_experts(c, k, attn, dst, nullptr, nullptr, n, s, 1, last);
+            if (!rc) rc = timer_mark(c, tm, 0, s);
+            if (!rc) rc = enqueue_experts(c, k, attn, dst, nullptr, nullptr, n, s, 1, last);
+            if (!rc) rc = timer_mark(c, tm, 1, s);
             if (rc) return rc;
         }
         src = dst;
@@ -1054,11 +1082,81 @@ extern "C" int prism_forward_e2e_graph(prism_ctx* c, const void* frame, void* di
     return run_forward_graph(c, frame, display, batch, stream, CHAIN_E2E);
 }
 
+extern "C" int prism_chain_launch_times(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream,
+                                        float* attn_ms, float* expert_ms, int32_t* attn_grid,
+                                        int32_t* expert_grid) {
+    int rc = forward_checks(c, in, out, batch);
+    if (rc) return rc;
+    if (!attn_ms || !expert_ms) return fail(c, PRISM_ERR_INVALID, "attn_ms or expert_ms is NULL");
+    HIP_TRY(c, hipSetDevice(c->device));
+    rc = mode_ready(c, CHAIN_BLOCKS, batch);
+    if (rc) return rc;
+    const hipStream_t s = (hipStream_t)stream;
+    rc = clean_counts(c, s);
+    if (rc) return rc;
+    ChainWs ws = c->wsb;
+    const int64_t T = (int64_t)c->desc.spatial_h * c->desc.spatial_w, D = c->desc.dim;
+    ws.n = (int64_t)batch * T;
+    c->fwd_tokens = ws.n;
+    c->fwd_assign = ws.assign;
+    /* the sub-chains of prism_forward, one after another on one stream */
+    const int S = std::max(1, std::min(CHAIN_SPLIT, batch / CHAIN_SPLIT_FRAMES));
+    ChainTimer tm;
+    tm.ev.assign((size_t)2 * c->desc.n_blocks * S + 1, nullptr);
+    for (auto& e : tm.ev) {
+        const hipError_t he = hipEventCreate(&e);
+        if (he != hipSuccess) {
+            for (auto& x : tm.ev)
+                if (x) (void)hipEventDestroy(x);
+            return fail(c, PRISM_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(he));
+        }
+    }
+    const uint16_t* src = static_cast<const uint16_t*>(in);
+    uint16_t* dst = static_cast<uint16_t*>(out);
+    rc = timer_mark(c, &tm, -1, s);
+    for (int j = 0; j < S && !rc; ++j) {
+        const int f0 = (int)((int64_t)batch * j / S), f1 = (int)((int64_t)batch * (j + 1) / S);
+        rc = enqueue_subchain(c, ws, j, f0, f1 - f0, src + f0 * T * D, dst + f0 * T * D, s, false, &tm);
+    }
+    if (rc) c->counts_dirty = true; /* launched part of the chain */
+    double sum[2] = {0, 0};
+    int cnt[2] = {0, 0};
+    unsigned grid[2] = {0, 0};
+    if (!rc) {
+        const hipError_t he = hipEventSynchronize(tm.ev[tm.n - 1]);
+        if (he != hipSuccess) rc = fail(c, PRISM_ERR_HIP, "hipEventSynchronize: %s", hipGetErrorString(he));
+        for (size_t i = 1; i < tm.n && !rc; ++i) {
+            float ms = 0.f;
+            const hipError_t ee = hipEventElapsedTime(&ms, tm.ev[i - 1], tm.ev[i]);
+            if (ee != hipSuccess) {
+                rc = fail(c, PRISM_ERR_HIP, "hipEventElapsedTime: %s", hipGetErrorString(ee));
+                break;
+            }
+            const int k = tm.kind[i - 1];
+            sum[k] += ms;
+            if (!cnt[k]++) grid[k] = tm.grid[i - 1];
+        }
+    }
+    for (auto& e : tm.ev) (void)hipEventDestroy(e);
+    if (rc) return rc;
+    *attn_ms = (float)(sum[0] / std::max(1, cnt[0]));
+    *expert_ms = (float)(sum[1] / std::max(1, cnt[1]));
+    if (attn_grid) *attn_grid = (int32_t)grid[0];
+    if (expert_grid) *expert_grid = (int32_t)grid[1];
+    return PRISM_OK;
+}
+
 /* The eager chain with its workspace in this device's scratch array instead
  * of the context's allocation: no hipMalloc / hipFree, ever. The counter rows
  * are cleared by a fill launch first (the array keeps the previous call's
- * contents); everything else is written before it is read. Calls that
- * overlap on one GPU share the array and race. */
+ * contents); everything else is written before it is read. Calls on one GPU,
+ * from any context and stream, run one after another: the call's stream waits
+ * for the device's completion event of the previous call, and the call
+ * records it after its own launches (under a host lock, so concurrent callers
+ * cannot interleave those steps). Under stream capture the wait and record
+ * are left out (an event recorded outside a capture cannot be waited on
+ * inside it): the captured graph's launches are then ordered by the stream the
+ * caller replays it on. */
 extern "C" int prism_forward_noalloc(prism_ctx* c, const void* in, void* out, int32_t batch, void* stream) {
     int rc = forward_checks(c, in, out, batch);
     if (rc) return rc;
@@ -1075,11 +1173,25 @@ extern "C" int prism_forward_noalloc(prism_ctx* c, const void* in, void* out, in
     const hipStream_t s = (hipStream_t)stream;
     const ChainWs ws = chain_ws_at(c->scratch, L, n, false);
     const int N = c->desc.n_experts, NB = c->desc.n_blocks;
+    const hipEvent_t done = scratch_done_event(c->device);
+    if (!done) return fail(c, PRISM_ERR_STATE, "no scratch completion event on device %d", c->device);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(c, hipStreamIsCapturing(s, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(scratch_call_mutex(c->device));
+    if (!capturing) HIP_TRY(c, hipStreamWaitEvent(s, done, 0));
     if (N > 1) {
         rc = enqueue_zero(c, ws.counts, CHAIN_SPLIT * NB * N * CHAIN_COUNT_STRIDE, s);
         if (rc) return rc;
     }
-    return enqueue_forward_impl(c, ws, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, s);
+    rc = enqueue_forward_impl(c, ws, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), batch, s);
+    /* recorded even after a failed enqueue: the event then covers whatever
+     * part of the chain was launched */
+    if (!capturing) {
+        const hipError_t e = hipEventRecord(done, s);
+        if (!rc && e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(e));
+    }
+    return rc;
 }
 
 extern "C" int prism_forward_assignments(prism_ctx* c, const int32_t** assign_dev, int64_t* tokens_per_block) {

@@ -128,6 +128,8 @@ SIGNATURES = {
     "prism_forward_graph": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
     "prism_forward_noalloc": (C.c_int, [_P, _P, _P, C.c_int32, _P]),
     "prism_forward_assignments": (C.c_int, [_P, C.POINTER(_P), C.POINTER(C.c_int64)]),
+    "prism_chain_launch_times": (C.c_int, [_P, _P, _P, C.c_int32, _P, C.POINTER(C.c_float), C.POINTER(C.c_float),
+                                           C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "prism_aux_elems": (C.c_int64, [C.c_int32, C.c_int64]),
     "prism_adapter_layout": (C.c_int, [C.POINTER(ModelDesc), C.c_int32, C.c_int64, C.POINTER(AdapterOffsets),
                                        C.POINTER(C.c_int64)]),
@@ -387,6 +389,12 @@ class Hip:
         L.hipGetErrorString.argtypes = [C.c_int]
         L.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
         L.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        L.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        L.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        L.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+        L.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        L.hipGraphDestroy.argtypes = [C.c_void_p]
+        L.hipGraphExecDestroy.argtypes = [C.c_void_p]
 
     def _ok(self, rc, what):
         if rc != 0:
@@ -444,6 +452,30 @@ class Hip:
 
     def record(self, ev: int, stream: int | None):
         self._ok(self.L.hipEventRecord(C.c_void_p(ev), C.c_void_p(stream or 0)), "hipEventRecord")
+
+    CAPTURE_GLOBAL = 0  # hipStreamCaptureModeGlobal
+
+    def begin_capture(self, stream: int, mode: int = CAPTURE_GLOBAL):
+        self._ok(self.L.hipStreamBeginCapture(C.c_void_p(stream), mode), "hipStreamBeginCapture")
+
+    def end_capture(self, stream: int) -> int:
+        """The captured graph (raises if the capture was invalidated)."""
+        g = C.c_void_p()
+        self._ok(self.L.hipStreamEndCapture(C.c_void_p(stream), C.byref(g)), "hipStreamEndCapture")
+        return g.value
+
+    def graph_instantiate(self, graph: int) -> int:
+        x = C.c_void_p()
+        self._ok(self.L.hipGraphInstantiate(C.byref(x), C.c_void_p(graph), None, None, 0), "hipGraphInstantiate")
+        return x.value
+
+    def graph_launch(self, graph_exec: int, stream: int):
+        self._ok(self.L.hipGraphLaunch(C.c_void_p(graph_exec), C.c_void_p(stream)), "hipGraphLaunch")
+
+    def graph_destroy(self, graph: int, graph_exec: int | None = None):
+        if graph_exec:
+            self._ok(self.L.hipGraphExecDestroy(C.c_void_p(graph_exec)), "hipGraphExecDestroy")
+        self._ok(self.L.hipGraphDestroy(C.c_void_p(graph)), "hipGraphDestroy")
 
     def elapsed_ms(self, a: int, b: int) -> float:
         self._ok(self.L.hipEventSynchronize(C.c_void_p(b)), "hipEventSynchronize")
@@ -576,6 +608,15 @@ class Engine:
     def project_push(self, up: bool, n_tokens: int, in_off: int, out_off: int) -> ProjectPush:
         a = self.aoffs
         return ProjectPush(n_tokens, 0, a.up_w if up else a.down_w, a.up_b if up else a.down_b, in_off, out_off)
+
+    def chain_launch_times(self, x: int, y: int, batch: int, stream: int | None = None):
+        """prism_chain_launch_times: (attention ms, expert ms, attention grid,
+        expert grid), the means over the chain's launches run one by one."""
+        a, e = C.c_float(), C.c_float()
+        ga, ge = C.c_int32(), C.c_int32()
+        _check(self.L.prism_chain_launch_times(self.h, x, y, batch, stream, C.byref(a), C.byref(e), C.byref(ga),
+                                               C.byref(ge)), self.h)
+        return a.value, e.value, ga.value, ge.value
 
     def forward_assignments(self):
         p = C.c_void_p()

@@ -15,6 +15,7 @@ import pytest
 import oracle as O
 import prism_amd as P
 from conftest import errors
+from test_gpu_ln_affine import with_affine
 
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
@@ -30,10 +31,15 @@ def adapters_f32(desc, blob, a):
             w[a.down_w:a.down_w + I * D].reshape(I, D), w[a.down_b:a.down_b + I])
 
 
-def setup(engine, name, nb, H, W, seed=0):
+def setup(engine, name, nb, H, W, seed=0, affine=False):
+    """Model + adapters loaded; affine: random LN gammas and betas in every
+    block (LN1 beta != 0 sends windows with padded slots through the attention
+    kernels' PAD bodies, also in the first block with the fused up-projection)."""
     cfg = P.CONFIGS[name]
     desc = cfg.desc(n_blocks=nb, H=H, W=W)
     blob, offs = P.synth_weights(desc, seed=seed, routing=cfg.routing)
+    if affine:
+        blob = with_affine(blob, offs, cfg.dim, seed=seed + 7)
     engine.load_weights(desc, blob, offs)
     ablob, a = P.synth_adapters(desc, seed=seed + 100)
     engine.load_adapters(ablob, a)
@@ -109,16 +115,21 @@ def test_adapted_chain_needs_adapters(hip, device_arena):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,nb,H,W,batch", [("moe64", 4, 68, 120, 1), ("dense128", 3, 68, 120, 2),
-                                               ("moe16", 2, 20, 28, 3), ("moe16", 2, 20, 28, 4)])
-def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch):
-    cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W)
+@pytest.mark.parametrize("name,nb,H,W,batch,affine", [
+    ("moe64", 4, 68, 120, 1, False), ("dense128", 3, 68, 120, 2, False),
+    ("moe16", 2, 20, 28, 3, False), ("moe16", 2, 20, 28, 4, False),
+    # LN affines: PAD and PAD+HALF bodies (the 68-row grid's bottom windows)
+    # with the fused up-projection in block 0, 8-wave and 4-wave kernels
+    ("moe64", 3, 68, 120, 1, True), ("moe64", 2, 68, 120, 4, True), ("dense128", 2, 68, 120, 2, True),
+])
+def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch, affine):
+    cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W, affine=affine)
     up_w, up_b, dn_w, dn_b = adapters_f32(desc, ablob, a)
     n, I = batch * H * W, a.in_dim
     x = P.synth_normal(n * I, seed=12).reshape(n, I)
     dx, dy, dz = device_arena(n * I * 2), device_arena(n * I * 2), device_arena(n * I * 2)
     hip.upload(dx.ptr, x)
-    print(f"[adapted] {name} {nb} blocks {H}x{W} batch {batch}", flush=True)
+    print(f"[adapted] {name} {nb} blocks {H}x{W} batch {batch} affine={affine}", flush=True)
     engine.forward(dx.ptr, dy.ptr, batch, adapted=True)
     hip.sync()
     y = hip.download(np.empty(n * I, np.uint16), dy.ptr)
@@ -138,25 +149,32 @@ def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,nb,H,W,batch", [
-    ("moe16", 2, 20, 28, 4),    # two sub-chains; ragged windows
-    ("moe64", 1, 68, 120, 1),   # one block: up- and down-projection in the same block
-    ("moe64", 3, 68, 120, 1),   # 8-wave kernels
-    ("dense128", 3, 68, 120, 2),
-    ("std256", 2, 16, 16, 5),   # dense d256, sub-chains of 2 and 3 frames
+@pytest.mark.parametrize("name,nb,H,W,batch,affine", [
+    ("moe16", 2, 20, 28, 4, False),    # two sub-chains; ragged windows
+    ("moe64", 1, 68, 120, 1, False),   # one block: up- and down-projection in the same block
+    ("moe64", 3, 68, 120, 1, False),   # 8-wave kernels
+    ("dense128", 3, 68, 120, 2, False),
+    ("std256", 2, 16, 16, 5, False),   # dense d256, sub-chains of 2 and 3 frames
+    # LN affines (LN1 beta != 0): block 0's windows with padded slots run the
+    # PAD / PAD+HALF bodies with the fused up-projection; every window of
+    # every block equals the separate calls bit for bit
+    ("moe64", 2, 68, 120, 1, True),    # 8 waves
+    ("moe64", 2, 68, 120, 4, True),    # 4 waves
+    ("moe16", 1, 20, 28, 4, True),     # ragged right and bottom windows, one block
+    ("dense128", 2, 68, 120, 2, True),
 ])
-def test_fused_adapters_equal_the_separate_calls(hip, engine, device_arena, name, nb, H, W, batch):
+def test_fused_adapters_equal_the_separate_calls(hip, engine, device_arena, name, nb, H, W, batch, affine):
     """The adapted chain fuses the up-projection into the first block's
     attention prologue and the down-projection into the last block's expert
     epilogue, with the projection kernels' arithmetic: its output is
     bit-identical to prism_project_up -> the plain chain -> prism_project_down."""
-    cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W)
+    cfg, desc, blob, offs, ablob, a = setup(engine, name, nb, H, W, affine=affine)
     n, D, I = batch * H * W, cfg.dim, a.in_dim
     x = P.synth_normal(n * I, seed=13).reshape(n, I)
     feats = device_arena((n * I + 2 * n * D + n * I) * 2 + 64)
     o_x, o_h, o_g, o_y = 0, n * I, n * I + n * D, n * I + 2 * n * D
     hip.upload(feats.ptr, x)
-    print(f"[fused] {name} {nb} blocks {H}x{W} batch {batch}", flush=True)
+    print(f"[fused] {name} {nb} blocks {H}x{W} batch {batch} affine={affine}", flush=True)
     assert engine.project(True, engine.project_push(True, H * W, o_x, o_h), feats.ptr, batch) == 0, engine.error()
     engine.forward(feats.ptr + o_h * 2, feats.ptr + o_g * 2, batch)
     assert engine.project(False, engine.project_push(False, H * W, o_g, o_y), feats.ptr, batch) == 0, engine.error()

@@ -16,6 +16,7 @@ import pytest
 import oracle as O
 import prism_amd as P
 from conftest import errors
+from test_gpu_ln_affine import with_affine
 
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
@@ -32,12 +33,15 @@ def f16(a):
     return a.astype(np.float16).astype(np.float32)
 
 
-def setup(engine, render, name="moe16", nb=1, seed=4):
-    """A model whose token grid is the render size encoded three times, and its codec."""
+def setup(engine, render, name="moe16", nb=1, seed=4, affine=False):
+    """A model whose token grid is the render size encoded three times, and its
+    codec; affine: random LN gammas and betas in every block."""
     cfg = P.CONFIGS[name]
     r = P.codec_resolutions(*render)
     desc = cfg.desc(n_blocks=nb, H=r[3][1], W=r[3][0])
     blob, offs = P.synth_weights(desc, seed=seed, routing=cfg.routing)
+    if affine:
+        blob = with_affine(blob, offs, cfg.dim, seed=seed + 7)
     engine.load_weights(desc, blob, offs)
     cblob, c, a = P.synth_codec(desc, seed=seed + 1, render_w=render[0], render_h=render[1])
     engine.load_codec(cblob, c)
@@ -154,10 +158,14 @@ def test_encode_decode_against_the_oracle_chain(hip, engine, device_arena):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,render,nb,batch", [("moe16", (130, 90), 2, 1), ("moe64", (960, 540), 2, 1),
-                                                   ("moe16", (130, 90), 2, 4)])
-def test_e2e_frame_equals_the_calls_it_chains(hip, engine, device_arena, name, render, nb, batch):
-    desc, r, W, _, (cblob, c, a) = setup(engine, render, name=name, nb=nb)
+@pytest.mark.parametrize("name,render,nb,batch,affine", [
+    ("moe16", (130, 90), 2, 1, False), ("moe64", (960, 540), 2, 1, False), ("moe16", (130, 90), 2, 4, False),
+    # LN affines: the 68-row token grid's bottom windows take the PAD+HALF body
+    # with the fused up-projection in block 0
+    ("moe64", (960, 540), 2, 1, True), ("moe64", (960, 540), 1, 4, True),
+])
+def test_e2e_frame_equals_the_calls_it_chains(hip, engine, device_arena, name, render, nb, batch, affine):
+    desc, r, W, _, (cblob, c, a) = setup(engine, render, name=name, nb=nb, affine=affine)
     (w0, h0), _, _, (w3, h3) = r
     rng = np.random.default_rng(9)
     n_in, n_out, n_tok = batch * 9 * h0 * w0, batch * 12 * h0 * w0, batch * h3 * w3 * 128
@@ -165,7 +173,7 @@ def test_e2e_frame_equals_the_calls_it_chains(hip, engine, device_arena, name, r
     df, dd, de = device_arena(n_in * 2), device_arena(n_out * 2), device_arena(n_out * 2)
     db, dc = device_arena(n_tok * 2), device_arena(n_tok * 2)
     hip.upload(df.ptr, frames)
-    print(f"[e2e] {name} {render} batch {batch}", flush=True)
+    print(f"[e2e] {name} {render} batch {batch} affine={affine}", flush=True)
     engine.encode(df.ptr, db.ptr, batch)
     engine.forward(db.ptr, dc.ptr, batch, adapted=True)
     engine.decode(dc.ptr, dd.ptr, batch)

@@ -28,30 +28,40 @@ def f16(bits):
     return O.f16bits_to_f32(bits)
 
 
-def with_affine(blob, offs, dim, seed):
-    """A copy of `blob` with random LN1/LN2 gamma and beta in every block."""
+def with_affine(blob, offs, dim, seed, small_gamma=False):
+    """A copy of `blob` with random LN1/LN2 gamma and beta in every block:
+    gamma ~ N(1, 0.3), or with small_gamma |gamma| ~ U(1e-3, 1e-2) with a
+    random sign (the folded W' = r16(W gamma) then lies in fp16's subnormal
+    range, ~2e-5 for W ~ N(0, 0.02), where it keeps fewer significant bits);
+    beta ~ N(0, 0.2)."""
     rng = np.random.default_rng(seed)
     out = blob.copy()
     for o in offs:
         for g_off, b_off in ((o.ln1_g, o.ln1_b), (o.ln2_g, o.ln2_b)):
-            out[g_off:g_off + dim] = O.f32_to_f16bits(rng.normal(1.0, 0.3, dim).astype(np.float32))
+            if small_gamma:
+                g = rng.uniform(1e-3, 1e-2, dim) * rng.choice([-1.0, 1.0], dim)
+            else:
+                g = rng.normal(1.0, 0.3, dim)
+            out[g_off:g_off + dim] = O.f32_to_f16bits(g.astype(np.float32))
             out[b_off:b_off + dim] = O.f32_to_f16bits(rng.normal(0.0, 0.2, dim).astype(np.float32))
     return out
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,batch,kernel", [
-    ("moe64", 1, "prism_attn_d256_w8_r4"),   # 135 windows: 8 waves
-    ("moe64", 4, "prism_attn_d256_r4"),      # 540 windows: 4 waves
-    ("moe24d128", 2, "prism_attn_d128_w8_r2"),
+@pytest.mark.parametrize("name,batch,kernel,small_gamma", [
+    ("moe64", 1, "prism_attn_d256_w8_r4", False),   # 135 windows: 8 waves
+    ("moe64", 4, "prism_attn_d256_r4", False),      # 540 windows: 4 waves
+    ("moe24d128", 2, "prism_attn_d128_w8_r2", False),
+    ("moe64", 1, "prism_attn_d256_w8_r4", True),    # folded weights in fp16's subnormal range
+    ("moe64", 4, "prism_attn_d256_r4", True),
 ])
-def test_routed_block_with_affine(hip, engine, device_arena, name, batch, kernel):
+def test_routed_block_with_affine(hip, engine, device_arena, name, batch, kernel, small_gamma):
     cfg = P.CONFIGS[name] if name in P.CONFIGS else P.Config(name, 128, 2, 8, 16, 24, 68, 120, 1, P.ROUTE_ZIPF)
     H, W, N, d = cfg.H, cfg.W, cfg.n_experts, cfg.dim
     n = batch * H * W
     desc = cfg.desc(n_blocks=1)
     blob0, offs = P.synth_weights(desc, seed=5, routing=cfg.routing)
-    blob = with_affine(blob0, offs, d, seed=7)
+    blob = with_affine(blob0, offs, d, seed=7, small_gamma=small_gamma)
     engine.load_weights(desc, blob, offs)
     w = f16(blob)
     c = O.cfg(d, cfg.n_heads, cfg.head_dim, N, H, W, batch, True)
@@ -60,7 +70,7 @@ def test_routed_block_with_affine(hip, engine, device_arena, name, batch, kernel
     aux_n = P.aux_elems(N, n)
     aux = device_arena(aux_n * 4)
     hip.upload(feats.ptr, O.f32_to_f16bits(x))
-    print(f"[affine] {name} batch {batch} ({kernel})", flush=True)
+    print(f"[affine] {name} batch {batch} ({kernel}) small gamma {small_gamma}", flush=True)
     pa = engine.attn_push(0, 0, n * d)
     pr = engine.router_push(0, H * W, n * d, 0, n, n + N)
     assert engine.attn_route(pa, pr, feats.ptr, aux.ptr, batch) == 0, engine.error()
@@ -101,21 +111,22 @@ def test_routed_block_with_affine(hip, engine, device_arena, name, batch, kernel
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,batch", [("std256", 1), ("dense128", 2)])
-def test_dense_block_with_affine(hip, engine, device_arena, name, batch):
+@pytest.mark.parametrize("name,batch,small_gamma", [("std256", 1, False), ("dense128", 2, False),
+                                                    ("std256", 1, True)])
+def test_dense_block_with_affine(hip, engine, device_arena, name, batch, small_gamma):
     cfg = P.CONFIGS[name]
     H, W, d = cfg.H, cfg.W, cfg.dim
     n = batch * H * W
     desc = cfg.desc(n_blocks=1)
     blob0, offs = P.synth_weights(desc, seed=9, routing=cfg.routing)
-    blob = with_affine(blob0, offs, d, seed=10)
+    blob = with_affine(blob0, offs, d, seed=10, small_gamma=small_gamma)
     engine.load_weights(desc, blob, offs)
     w = f16(blob)
     c = O.cfg(d, cfg.n_heads, cfg.head_dim, 1, H, W, batch, True)
     x = f16(P.synth_features(cfg, batch=batch, H=H, W=W, seed=11).reshape(n, d))
     feats = device_arena(3 * n * d * 2)
     hip.upload(feats.ptr, O.f32_to_f16bits(x))
-    print(f"[affine] {name} batch {batch}", flush=True)
+    print(f"[affine] {name} batch {batch} small gamma {small_gamma}", flush=True)
     assert engine.attn(engine.attn_push(0, 0, n * d), feats.ptr, batch) == 0, engine.error()
     hip.sync()
     h_gpu = f16(hip.download(np.empty(n * d, np.uint16), feats.ptr + n * d * 2)).reshape(n, d)
