@@ -320,6 +320,14 @@ bool prism::codec_resolutions(const prism_model_desc* d, int render_w, int rende
         if (why) *why = "render size " + std::to_string(render_w) + "x" + std::to_string(render_h) + " out of range";
         return false;
     }
+    /* the conv stages address a frame's maps with 32-bit byte offsets; the
+     * largest is the 32-channel fp16 map at the render size (64 B a pixel) */
+    if ((int64_t)render_w * render_h * 64 > (int64_t)0x7fffffff) {
+        if (why)
+            *why = "render size " + std::to_string(render_w) + "x" + std::to_string(render_h) +
+                   " too large: its 32-channel map exceeds 2 GiB per frame";
+        return false;
+    }
     rw[0] = render_w;
     rh[0] = render_h;
     for (int i = 1; i < 4; ++i) { /* a 3x3 stride-2 conv with padding 1 */

@@ -127,14 +127,14 @@ typedef struct CodecArgs {
 /* enc0 output block per workgroup (rows x columns) */
 #define CODEC_ENC0_ROWS 4
 #define CODEC_ENC0_COLS 64
-#define CODEC_TT_ENC2 1
-#define CODEC_TT_ENC3 2
+#define CODEC_TT_ENC2 2
+#define CODEC_TT_ENC3 1
 #define CODEC_TT_DEC3 2
-#define CODEC_TT_DEC2 4
-#define CODEC_TT_DEC1 4
+#define CODEC_TT_DEC2 3
+#define CODEC_TT_DEC1 2
 #define CODEC_RS_ENC1 1
 #define CODEC_RS_ENC2 1
-#define CODEC_RS_ENC3 4
+#define CODEC_RS_ENC3 2
 #define CODEC_RS_DEC3 1
 #define CODEC_RS_DEC2 1
 

@@ -36,8 +36,8 @@
  * Workgroup = 4 waves; wave w takes TT consecutive 16-pixel tiles (pixels in
  * row-major order of the output map, blockIdx.y = frame) and all COUT output
  * channels. Each k-step's weight fragments and B fragments are loaded one
- * k-step ahead of its MFMAs. Loads at padded or out-of-map positions read a
- * clamped in-map address and are replaced by zeros.
+ * k-step ahead of its MFMAs. Loads at padded or out-of-map positions return
+ * zeros through the input buffer's range check (MapSrc).
  */
 #pragma once
 #include "common.hpp"
@@ -48,20 +48,49 @@ struct CodecPix {
     bool valid;
 };
 
-/* conv3x3 (pad 1) over an NHWC map with CIN channels; k = tap*CIN + ic. */
+/* The B gathers read a frame's map through a buffer resource whose range is
+ * the map: a lane whose operand is zero (a tap in the conv padding) or
+ * unused (a pixel past the map's end, whose output column is never stored)
+ * gets the offset CODEC_OOB, and the range check returns zeros for it. Each
+ * lane's byte offsets are 32-bit (the host keeps a frame's largest map under
+ * 2 GiB) and computed once per token tile, so a load is one instruction with
+ * its k-step's channel offset in the immediate field. */
+static constexpr uint32_t CODEC_OOB = 0x80000000u;
+struct MapSrc {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ __forceinline__ MapSrc(const uint16_t* base, uint32_t bytes)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000)) {}
+    __device__ __forceinline__ h8 load(uint32_t off) const {
+        return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    }
+};
+
+/* conv3x3 (pad 1) over an NHWC map with CIN channels; k = tap*CIN + ic. A
+ * tile's per-lane state: the byte offset of each of the 9 taps' input pixel
+ * (channel 8g), CODEC_OOB where the tap falls in the padding. */
 template <int CIN, int STRIDE>
 struct SrcConvNHWC {
     static constexpr int KS = 9 * CIN / 32;
-    const uint16_t* in;
+    MapSrc m;
     int iw, ih;
-    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
+    struct Pix {
+        uint32_t off[9];
+    };
+    __device__ __forceinline__ Pix prep(const CodecPix& p, int g) const {
+        Pix q;
+        const int iy0 = p.y * STRIDE - 1, ix0 = p.x * STRIDE - 1;
+        const int base = ((iy0 * iw + ix0) * CIN + 8 * g) * 2; /* may be negative: only in-map taps use it */
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int iy = iy0 + tap / 3, ix = ix0 + tap % 3;
+            const bool ok = p.valid && iy >= 0 && iy < ih && ix >= 0 && ix < iw;
+            q.off[tap] = ok ? (uint32_t)(base + ((tap / 3) * iw + tap % 3) * CIN * 2) : CODEC_OOB;
+        }
+        return q;
+    }
+    __device__ __forceinline__ h8 load(int ks, const Pix& q) const {
         constexpr int CPT = CIN / 32; /* k-steps per tap */
-        const int tap = ks / CPT, c0 = (ks % CPT) * 32 + 8 * g;
-        const int iy = p.y * STRIDE + tap / 3 - 1, ix = p.x * STRIDE + tap % 3 - 1;
-        const bool ok = p.valid && iy >= 0 && iy < ih && ix >= 0 && ix < iw;
-        const int64_t pix = ok ? (int64_t)iy * iw + ix : 0;
-        const h8 v = *reinterpret_cast<const h8*>(in + pix * CIN + c0);
-        return ok ? v : h8{};
+        return m.load(q.off[ks / CPT] + (uint32_t)((ks % CPT) * 64));
     }
 };
 
@@ -71,19 +100,19 @@ struct SrcConvNHWC {
 template <int CUP, int CSKIP>
 struct SrcDec {
     static constexpr int KS = (CUP + CSKIP) / 32;
-    const uint16_t* up;
-    const uint16_t* skip;
+    MapSrc mu, ms;
     int uw, uh, ow;
-    __device__ __forceinline__ h8 load(int ks, const CodecPix& p, int g) const {
-        const int y = p.valid ? p.y : 0, x = p.valid ? p.x : 0;
-        h8 v;
-        if (32 * ks < CUP) {
-            const int uy = min(y >> 1, uh - 1), ux = min(x >> 1, uw - 1);
-            v = *reinterpret_cast<const h8*>(up + ((int64_t)uy * uw + ux) * CUP + 32 * ks + 8 * g);
-        } else {
-            v = *reinterpret_cast<const h8*>(skip + ((int64_t)y * ow + x) * CSKIP + 32 * ks - CUP + 8 * g);
-        }
-        return p.valid ? v : h8{};
+    struct Pix {
+        uint32_t up, skip;
+    };
+    __device__ __forceinline__ Pix prep(const CodecPix& p, int g) const {
+        const int uy = min(p.y >> 1, uh - 1), ux = min(p.x >> 1, uw - 1);
+        return Pix{p.valid ? (uint32_t)(((uy * uw + ux) * CUP + 8 * g) * 2) : CODEC_OOB,
+                   p.valid ? (uint32_t)(((p.y * ow + p.x) * CSKIP + 8 * g) * 2) : CODEC_OOB};
+    }
+    __device__ __forceinline__ h8 load(int ks, const Pix& q) const {
+        if (32 * ks < CUP) return mu.load(q.up + (uint32_t)(64 * ks));
+        return ms.load(q.skip + (uint32_t)(64 * ks - 2 * CUP));
     }
 };
 
@@ -101,16 +130,19 @@ __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, co
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = bb;
     }
+    typename Src::Pix q[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) q[t] = src.prep(px[t], g);
     h8 bc[TT], bn[TT], wc[RT], wn[RT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) bc[t] = src.load(0, px[t], g);
+    for (int t = 0; t < TT; ++t) bc[t] = src.load(0, q[t]);
 #pragma unroll
     for (int r = 0; r < RT; ++r) wc[r] = wsrc.load((rt0 + r) * KS, lane * 16);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) {
 #pragma unroll
-            for (int t = 0; t < TT; ++t) bn[t] = src.load(ks + 1, px[t], g);
+            for (int t = 0; t < TT; ++t) bn[t] = src.load(ks + 1, q[t]);
 #pragma unroll
             for (int r = 0; r < RT; ++r) wn[r] = wsrc.load((rt0 + r) * KS + ks + 1, lane * 16);
         }
@@ -193,7 +225,8 @@ __device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
     CodecPix px[TT];
     codec_pixels<TT, 1>(a, wave, l16, px);
     const int f = blockIdx.y;
-    const SrcDec<64, 32> src{a.in + (int64_t)f * a.in_frame, a.skip + (int64_t)f * a.skip_frame, a.in_w, a.in_h,
+    const SrcDec<64, 32> src{MapSrc(a.in + (int64_t)f * a.in_frame, (uint32_t)(a.in_frame * 2)),
+                             MapSrc(a.skip + (int64_t)f * a.skip_frame, (uint32_t)(a.skip_frame * 2)), a.in_w, a.in_h,
                              a.out_w};
     f4 acc[2][TT];
     codec_gemm<SrcDec<64, 32>, 2, 2, TT>(src, a.w, a.b, px, g, lane, 0, acc);
@@ -309,24 +342,28 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
 }
 
 #define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))
+#define CODEC_IN_MAP MapSrc(CODEC_FRAME(a.in, a.in_frame), (uint32_t)(a.in_frame * 2))
+#define CODEC_SKIP_MAP MapSrc(CODEC_FRAME(a.skip, a.skip_frame), (uint32_t)(a.skip_frame * 2))
 
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
-    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc2(CodecArgs a) {
-    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc3(CodecArgs a) {
-    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_FRAME(a.in, a.in_frame), a.in_w, a.in_h});
+    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec3(CodecArgs a) {
     codec_stage<SrcDec<128, 128>, 128, CODEC_TT_DEC3, CODEC_RS_DEC3>(
-        a, SrcDec<128, 128>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
+        a, SrcDec<128, 128>{CODEC_IN_MAP, CODEC_SKIP_MAP, a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec2(CodecArgs a) {
     codec_stage<SrcDec<128, 64>, 64, CODEC_TT_DEC2, CODEC_RS_DEC2>(
-        a, SrcDec<128, 64>{CODEC_FRAME(a.in, a.in_frame), CODEC_FRAME(a.skip, a.skip_frame), a.in_w, a.in_h, a.out_w});
+        a, SrcDec<128, 64>{CODEC_IN_MAP, CODEC_SKIP_MAP, a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec1_out(CodecArgs a) { codec_dec_out<CODEC_TT_DEC1>(a); }
 #undef CODEC_FRAME
+#undef CODEC_IN_MAP
+#undef CODEC_SKIP_MAP
