@@ -1,7 +1,9 @@
 """Host-renderer interop through the C ABI: prism_init_with_device (the engine
 bound to the caller's stream), prism_infer_gpu (caller buffers at byte
 offsets, synchronous, GPU time returned) and renderer-owned memory imported
-from an exported file descriptor.
+from an exported file descriptor. The renderer-stream results equal
+prism_forward_graph's bit for bit and, for the plain chains, are also held to
+the free-running oracle directly.
 
 The exporter side of the last test stands in for a Vulkan renderer that
 exports a VkDeviceMemory with VK_KHR_external_memory_fd: a HIP allocation made
@@ -14,6 +16,7 @@ import os
 import numpy as np
 import pytest
 
+import oracle as O
 import prism_amd as P
 
 SENTINEL = 0x7E7E  # an fp16 NaN pattern no kernel writes
@@ -29,14 +32,29 @@ def _model(engine, name, nb, H, W, adapted, seed=2):
         ablob, a = P.synth_adapters(desc, seed=seed + 1)
         engine.load_adapters(ablob, a)
         ch = a.in_dim
-    return cfg, ch
+    return cfg, ch, desc, blob, offs
+
+
+def _oracle_check(cfg, desc, blob, offs, x_bits, y_bits, H, W, batch):
+    """The interop output against the free-running oracle of the same model,
+    with the whole-model bounds of the configuration tests (mean error 2e-3,
+    at most 2 % of tokens moved by more than 2e-2 by near-tie routing flips)."""
+    d = cfg.dim
+    c = O.cfg(d, cfg.n_heads, cfg.head_dim, cfg.n_experts, H, W, batch, True)
+    ref, _, _ = O.forward(c, O.f16bits_to_f32(blob), list(offs), O.f16bits_to_f32(x_bits).reshape(-1, d))
+    y = O.f16bits_to_f32(y_bits).reshape(-1, d).astype(np.float64)
+    err = np.abs(y - ref)
+    moved = float((err.max(axis=1) > 2e-2).mean())
+    print(f"[interop] oracle: max {err.max():.3g} mean {err.mean():.3g}, tokens moved {moved:.4f}", flush=True)
+    assert np.isfinite(y).all()
+    assert err.mean() <= 2e-3 and moved <= 0.02
 
 
 def _reference(hip, device_arena, name, nb, H, W, batch, adapted, x):
     """The same model through prism_forward_graph on plain device buffers."""
     eng = P.Engine(0)
     try:
-        _, ch = _model(eng, name, nb, H, W, adapted)
+        _, ch, _, _, _ = _model(eng, name, nb, H, W, adapted)
         n = batch * H * W * ch
         dx, dy = device_arena(n * 2), device_arena(n * 2)
         hip.upload(dx.ptr, x)
@@ -64,7 +82,7 @@ def test_infer_gpu_on_the_renderer_stream(hip, device_arena, name, nb, H, W, bat
     stream = hip.stream()
     eng = P.Engine(0, stream=stream)
     try:
-        _model(eng, name, nb, H, W, adapted)
+        _, _, desc, blob, offs = _model(eng, name, nb, H, W, adapted)
         in_off, out_off = 4096, 272  # byte offsets into the caller's buffers (16-byte aligned)
         tail = 512
         inb, outb = device_arena(in_off + n * 2 + tail), device_arena(out_off + n * 2 + tail)
@@ -82,6 +100,8 @@ def test_infer_gpu_on_the_renderer_stream(hip, device_arena, name, nb, H, W, bat
             print(f"[interop] call {rep}: {ms:.3f} ms", flush=True)
         x_after = hip.download(np.empty(n, np.uint16), inb.ptr + in_off)
         assert (x_after == x).all(), "the input was modified"
+        if not adapted:  # the adapted chain's oracle parity: test_gpu_adapters.py
+            _oracle_check(cfg, desc, blob, offs, x, got[out_off // 2:out_off // 2 + n], H, W, batch)
         # misaligned offset, overlapping ranges: refused before any launch
         with pytest.raises(P.PrismError) as ei:
             eng.infer_gpu(inb.ptr, in_off + 2, outb.ptr, out_off, batch)
