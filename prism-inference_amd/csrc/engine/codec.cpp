@@ -27,6 +27,7 @@ enum { ST_ENC0, ST_ENC1, ST_ENC2, ST_ENC3, ST_DEC3, ST_DEC2, ST_DEC1, N_STAGES }
 const int kTT[N_STAGES] = {4, CODEC_TT_ENC1, CODEC_TT_ENC2, CODEC_TT_ENC3, /* enc0: own grid */
                            CODEC_TT_DEC3, CODEC_TT_DEC2, CODEC_TT_DEC1};
 const int kRS[N_STAGES] = {1, CODEC_RS_ENC1, CODEC_RS_ENC2, CODEC_RS_ENC3, CODEC_RS_DEC3, CODEC_RS_DEC2, 1};
+const int kKSP[N_STAGES] = {1, CODEC_KSP_ENC1, CODEC_KSP_ENC2, CODEC_KSP_ENC3, CODEC_KSP_DEC3, CODEC_KSP_DEC2, 1};
 const int kInRes[N_STAGES] = {0, 0, 1, 2, 3, 2, 1};  /* resolution index of the (coarse) input map */
 const int kOutRes[N_STAGES] = {0, 1, 2, 3, 2, 1, 0}; /* of the output map (dec1: before the shuffle) */
 const int kInCh[N_STAGES] = {9, 32, 64, 128, 128, 128, 64};
@@ -57,7 +58,7 @@ int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip,
     a.in_frame = in_pix * kInCh[st];
     a.skip_frame = out_pix * kSkipCh[st];
     a.out_frame = out_pix * kOutCh[st];
-    const int64_t per_wg = 64 * kTT[st] / kRS[st];
+    const int64_t per_wg = 64 * kTT[st] / (kRS[st] * kKSP[st]); /* pixels per workgroup */
     const unsigned gx = st == ST_ENC0 ? (unsigned)(((a.out_w + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS) *
                                                   ((a.out_h + CODEC_ENC0_ROWS - 1) / CODEC_ENC0_ROWS))
                                       : (unsigned)((out_pix + per_wg - 1) / per_wg);

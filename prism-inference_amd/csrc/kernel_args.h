@@ -128,14 +128,22 @@ typedef struct CodecArgs {
 #define CODEC_ENC0_ROWS 4
 #define CODEC_ENC0_COLS 64
 #define CODEC_TT_ENC2 2
-#define CODEC_TT_ENC3 1
+#define CODEC_TT_ENC3 2
 #define CODEC_TT_DEC3 2
 #define CODEC_TT_DEC2 3
 #define CODEC_TT_DEC1 2
 #define CODEC_RS_ENC1 1
 #define CODEC_RS_ENC2 1
-#define CODEC_RS_ENC3 2
+#define CODEC_RS_ENC3 1
 #define CODEC_RS_DEC3 1
 #define CODEC_RS_DEC2 1
+/* KSP: how many waves of a pixel group split the stage's reduction (its
+ * k-steps) instead of its channels; a workgroup then covers
+ * 16 * TT * 4 / KSP pixels (RS is 1 for such a stage) */
+#define CODEC_KSP_ENC1 1
+#define CODEC_KSP_ENC2 1
+#define CODEC_KSP_ENC3 4
+#define CODEC_KSP_DEC3 1
+#define CODEC_KSP_DEC2 1
 
 #endif

@@ -33,9 +33,11 @@
  *         reference's out12 map), then sigmoid in fp32, fp16 again, written
  *         as 2x2 display pixels of the lane's RGB plane.
  *
- * Workgroup = 4 waves; wave w takes TT consecutive 16-pixel tiles (pixels in
+ * Workgroup = 4 waves; a wave takes TT consecutive 16-pixel tiles (pixels in
  * row-major order of the output map, blockIdx.y = frame) and all COUT output
- * channels. Each k-step's weight fragments and B fragments are loaded one
+ * channels, or 1/RS of them (channel split), or all of them over 1/KSP of
+ * the reduction (K-split, enc3). Each k-step's weight fragments and B
+ * fragments are loaded one
  * k-step ahead of its MFMAs. Loads at padded or out-of-map positions return
  * zeros through the input buffer's range check (MapSrc).
  */
@@ -88,9 +90,12 @@ struct SrcConvNHWC {
         }
         return q;
     }
-    __device__ __forceinline__ h8 load(int ks, const Pix& q) const {
+    /* k-step i KSP + j (i compile-time, j < KSP wave-uniform) */
+    template <int KSP>
+    __device__ __forceinline__ h8 load(int i, int j, const Pix& q) const {
         constexpr int CPT = CIN / 32; /* k-steps per tap */
-        return m.load(q.off[ks / CPT] + (uint32_t)((ks % CPT) * 64));
+        static_assert(CPT % KSP == 0, "a split's k-steps stay within one tap");
+        return m.load(q.off[i * KSP / CPT] + (uint32_t)(((i * KSP) % CPT + j) * 64));
     }
 };
 
@@ -110,23 +115,29 @@ struct SrcDec {
         return Pix{p.valid ? (uint32_t)(((uy * uw + ux) * CUP + 8 * g) * 2) : CODEC_OOB,
                    p.valid ? (uint32_t)(((p.y * ow + p.x) * CSKIP + 8 * g) * 2) : CODEC_OOB};
     }
-    __device__ __forceinline__ h8 load(int ks, const Pix& q) const {
-        if (32 * ks < CUP) return mu.load(q.up + (uint32_t)(64 * ks));
-        return ms.load(q.skip + (uint32_t)(64 * ks - 2 * CUP));
+    /* k-step i KSP + j (i compile-time, j < KSP wave-uniform) */
+    template <int KSP>
+    __device__ __forceinline__ h8 load(int i, int j, const Pix& q) const {
+        static_assert((CUP / 32) % KSP == 0, "a split's k-steps stay within one map");
+        if (32 * i * KSP < CUP) return mu.load(q.up + (uint32_t)(64 * (i * KSP + j)));
+        return ms.load(q.skip + (uint32_t)(64 * (i * KSP + j) - 2 * CUP));
     }
 };
 
 /* The GEMM: acc[r][t] = bias + W[16(rt0 + r).., :] * P[:, tile t] for RT row
- * tiles from rt0 (of the matrix's RTALL). */
-template <class Src, int RTALL, int RT, int TT>
+ * tiles from rt0 (of the matrix's RTALL), over the k-steps i KSP + kj
+ * (all of them for KSP = 1; a K-split stage's wave kj takes every KSP-th,
+ * and only kj = 0 starts at the bias). */
+template <class Src, int RTALL, int RT, int TT, int KSP = 1>
 __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, const float* bias, const CodecPix (&px)[TT],
-                                           int g, int lane, int rt0, f4 (&acc)[RT][TT]) {
-    constexpr int KS = Src::KS;
+                                           int g, int lane, int rt0, f4 (&acc)[RT][TT], int kj = 0) {
+    constexpr int KS = Src::KS, KN = KS / KSP;
+    static_assert(KS % KSP == 0, "whole k-steps per wave");
     const FragSrc wsrc(w, (unsigned)(RTALL * KS * 1024));
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const int ch = 16 * (rt0 + r) + 4 * g;
-        const f4 bb = {bias[ch], bias[ch + 1], bias[ch + 2], bias[ch + 3]};
+        const f4 bb = kj == 0 ? f4{bias[ch], bias[ch + 1], bias[ch + 2], bias[ch + 3]} : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = bb;
     }
@@ -135,22 +146,22 @@ __device__ __forceinline__ void codec_gemm(const Src& src, const uint16_t* w, co
     for (int t = 0; t < TT; ++t) q[t] = src.prep(px[t], g);
     h8 bc[TT], bn[TT], wc[RT], wn[RT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) bc[t] = src.load(0, q[t]);
+    for (int t = 0; t < TT; ++t) bc[t] = src.template load<KSP>(0, kj, q[t]);
 #pragma unroll
-    for (int r = 0; r < RT; ++r) wc[r] = wsrc.load((rt0 + r) * KS, lane * 16);
+    for (int r = 0; r < RT; ++r) wc[r] = wsrc.load((rt0 + r) * KS + kj, lane * 16);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) {
+    for (int ks = 0; ks < KN; ++ks) {
+        if (ks + 1 < KN) {
 #pragma unroll
-            for (int t = 0; t < TT; ++t) bn[t] = src.load(ks + 1, q[t]);
+            for (int t = 0; t < TT; ++t) bn[t] = src.template load<KSP>(ks + 1, kj, q[t]);
 #pragma unroll
-            for (int r = 0; r < RT; ++r) wn[r] = wsrc.load((rt0 + r) * KS + ks + 1, lane * 16);
+            for (int r = 0; r < RT; ++r) wn[r] = wsrc.load((rt0 + r) * KS + (ks + 1) * KSP + kj, lane * 16);
         }
 #pragma unroll
         for (int r = 0; r < RT; ++r)
 #pragma unroll
             for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wc[r], bc[t], acc[r][t]);
-        if (ks + 1 < KS) {
+        if (ks + 1 < KN) {
 #pragma unroll
             for (int t = 0; t < TT; ++t) bc[t] = bn[t];
 #pragma unroll
@@ -214,6 +225,88 @@ __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) 
         if (p0 + pl < npix)
             *reinterpret_cast<h8*>(out + (p0 + pl) * COUT + c8) = *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
     }
+}
+
+/* One stage with its reduction split over KSP waves (K-split): the
+ * workgroup's 4 waves form 4/KSP pixel groups of TT tiles; wave j of a group
+ * takes every KSP-th k-step from j for every output channel, so each wave's
+ * chain of dependent weight and operand round trips is KSP times shorter
+ * than the whole reduction (the deep stages' reductions are latency chains
+ * otherwise: few MFMAs per k-step, one round trip each). Wave j then owns
+ * row tiles [j RQ, (j+1) RQ) (RQ = RTALL/KSP): it publishes its partial
+ * tiles of the other rows in LDS, sums the group's KSP partials of its own
+ * rows in wave order (the first carries the bias), ReLU, fp16, into the
+ * output tile. */
+template <class Src, int COUT, int TT, int KSP>
+__device__ __forceinline__ void codec_stage_ksplit(const CodecArgs& a, const Src& src) {
+    constexpr int RTALL = COUT / 16, RQ = RTALL / KSP, NO = RTALL - RQ;
+    static_assert(COUT % 16 == 0 && 4 % KSP == 0 && RTALL % KSP == 0, "K-split shape");
+    constexpr int NPX = (4 / KSP) * TT * 16, LDO = COUT + 8;
+    __shared__ __attribute__((aligned(16))) f4 part[4 * NO * TT * 64]; /* [wave][row tile not owned][t][lane] */
+    __shared__ __attribute__((aligned(16))) f16 otile[NPX * LDO];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int pg = wave / KSP, kq = wave % KSP;
+    CodecPix px[TT];
+    codec_pixels<TT, KSP>(a, wave, l16, px);
+    f4 acc[RTALL][TT];
+    codec_gemm<Src, RTALL, RTALL, TT, KSP>(src, a.w, a.b, px, g, lane, 0, acc, kq);
+    /* the slot of row tile r (not owned by position j) of wave w; for an owned
+     * r (a value the reduction computes and does not use) a slot in range */
+    auto slot = [&](int w, int j, int r, int t) {
+        return ((w * NO + (r < j * RQ ? r : max(r - RQ, 0))) * TT + t) * 64 + lane;
+    };
+#pragma unroll
+    for (int r = 0; r < RTALL; ++r)
+        if (r / RQ != kq) /* uniform */
+#pragma unroll
+            for (int t = 0; t < TT; ++t) part[slot(wave, kq, r, t)] = acc[r][t];
+    __syncthreads();
+    const int pl0 = pg * TT * 16;
+    /* kq with its range hidden: knowing kq < KSP, the compiler turns the
+     * select chain below into a register index (private memory) */
+    int ksel = kq;
+    asm("" : "+s"(ksel));
+#pragma unroll
+    for (int rr = 0; rr < RQ; ++rr) {
+        const int r = kq * RQ + rr;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            f4 own = acc[rr][t]; /* acc[r][t], selected without indexing registers */
+#pragma unroll
+            for (int c = 1; c < KSP; ++c)
+                if (ksel == c) own = acc[c * RQ + rr][t];
+            f4 v = kq == 0 ? own : part[slot(pg * KSP, 0, r, t)];
+#pragma unroll
+            for (int j = 1; j < KSP; ++j) {
+                const f4 u = kq == j ? own : part[slot(pg * KSP + j, j, r, t)];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] += u[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(otile + (pl0 + 16 * t + l16) * LDO + 16 * r + 4 * g) = cvt_h4(v);
+        }
+    }
+    __syncthreads();
+    const int64_t p0 = (int64_t)blockIdx.x * NPX, npix = (int64_t)a.out_w * a.out_h;
+    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+    constexpr int CPP = COUT / 8;
+    for (int q = threadIdx.x; q < NPX * CPP; q += 256) {
+        const int pl = q / CPP, c8 = (q % CPP) * 8;
+        if (p0 + pl < npix)
+            *reinterpret_cast<h8*>(out + (p0 + pl) * COUT + c8) = *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
+    }
+}
+
+/* A stage's kernel body: K-split when KSP > 1, else channels split over RS
+ * waves. */
+template <class Src, int COUT, int TT, int RS, int KSP>
+__device__ __forceinline__ void codec_stage_any(const CodecArgs& a, const Src& src) {
+    static_assert(RS == 1 || KSP == 1, "a stage splits its channels or its reduction, not both");
+    if constexpr (KSP > 1) codec_stage_ksplit<Src, COUT, TT, KSP>(a, src);
+    else codec_stage<Src, COUT, TT, RS>(a, src);
 }
 
 /* dec1 + output conv + PixelShuffle(2) + sigmoid. */
@@ -347,20 +440,20 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
-    codec_stage<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
+    codec_stage_any<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1, CODEC_KSP_ENC1>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc2(CodecArgs a) {
-    codec_stage<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
+    codec_stage_any<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2, CODEC_KSP_ENC2>(a, SrcConvNHWC<64, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc3(CodecArgs a) {
-    codec_stage<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
+    codec_stage_any<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3, CODEC_KSP_ENC3>(a, SrcConvNHWC<128, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec3(CodecArgs a) {
-    codec_stage<SrcDec<128, 128>, 128, CODEC_TT_DEC3, CODEC_RS_DEC3>(
+    codec_stage_any<SrcDec<128, 128>, 128, CODEC_TT_DEC3, CODEC_RS_DEC3, CODEC_KSP_DEC3>(
         a, SrcDec<128, 128>{CODEC_IN_MAP, CODEC_SKIP_MAP, a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec2(CodecArgs a) {
-    codec_stage<SrcDec<128, 64>, 64, CODEC_TT_DEC2, CODEC_RS_DEC2>(
+    codec_stage_any<SrcDec<128, 64>, 64, CODEC_TT_DEC2, CODEC_RS_DEC2, CODEC_KSP_DEC2>(
         a, SrcDec<128, 64>{CODEC_IN_MAP, CODEC_SKIP_MAP, a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec1_out(CodecArgs a) { codec_dec_out<CODEC_TT_DEC1>(a); }
