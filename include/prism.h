@@ -345,7 +345,8 @@ int prism_load_model_file(prism_ctx* ctx, const char* weights_path, const char* 
  *            enc1 -> PW 192->64 (r1), dec1 NN-up + concat enc0 -> PW 96->32
  *            (r0), each + ReLU; output PW 32->12; PixelShuffle(2) + sigmoid
  *            -> RGB at 2 x r0.
- * r(i+1) = ceil(r(i) / 2) and r3 must be the model's spatial_h x spatial_w.
+ * r(i+1) = ceil(r(i) / 2) and r3 must be the model's spatial_h x spatial_w;
+ * render_w * render_h * 64 (the 32-channel fp16 map) must stay under 2^31.
  * Weight offsets (fp16 elements, 8-aligned), row-major [out][in] with the
  * reference's column orders: conv k = ic*9 + ky*3 + kx (enc*), concat order
  * upsampled channels first (dec*). */

@@ -287,3 +287,12 @@ def test_codec_layout_follows_the_reference_order():
     with pytest.raises(P.PrismError) as ei:
         P.codec_layout(desc, 960, 530)
     assert ei.value.code == P.ERR_INVALID and "encodes to" in P.lib().prism_last_error(None).decode()
+    # a render size whose 32-channel fp16 map would pass 2 GiB per frame (the conv stages'
+    # 32-bit map offsets), on a model whose grid it encodes to: 8192 x 4200 -> 1024 x 525
+    big = P.CONFIGS["moe64"].desc(H=525, W=1024)
+    with pytest.raises(P.PrismError) as ei:
+        P.codec_layout(big, 8192, 4200)
+    assert ei.value.code == P.ERR_INVALID and "2 GiB" in P.lib().prism_last_error(None).decode()
+    # 8192 x 4093 (encodes to 1024 x 512) stays under the limit: accepted
+    P.codec_layout(P.CONFIGS["moe64"].desc(H=512, W=1024), 8192, 4093)
+
