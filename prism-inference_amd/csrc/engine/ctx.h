@@ -54,6 +54,11 @@ static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
  * sub-chain's attention launch fills that round, and 128-token tiles stay
  * ahead there. */
 static constexpr int EXPERT_WIDE_MIN_TILES = 512;
+/* Workgroups of a projection stage launch (persistent, 64-token tiles in a
+ * loop; the d256 kernels' 210-220 VGPRs allow two per CU). At batch 16,
+ * 68x120, up 128->256: 512 workgroups 18.5 us, 384 20.6, 256 23.5, 1024
+ * 21.8 (one workgroup per tile: 20.5). */
+static constexpr int PROJ_GRID_MAX = 512;
 
 /* Attention keys all 64 slots of a window. The reference keys the first
  * min(64, n_tokens) slots in slot order (split2_qkv_attn_d256.comp.glsl:33,60),

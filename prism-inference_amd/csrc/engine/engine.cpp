@@ -586,8 +586,10 @@ int enqueue_project(prism_ctx* c, bool up, const uint16_t* in, uint16_t* out, in
     a.w = up ? c->up_w : c->down_w;
     a.b = up ? c->up_b : c->down_b;
     a.n_tokens = n;
-    const int64_t grid = (n + 63) / 64;
-    if (grid <= 0 || grid > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "projection grid %lld out of range", (long long)grid);
+    const int64_t tiles = (n + 63) / 64;
+    if (tiles <= 0 || tiles > 0x7fffffff) return fail(c, PRISM_ERR_INVALID, "projection tiles %lld out of range", (long long)tiles);
+    /* persistent workgroups, each looping over 64-token tiles */
+    const int64_t grid = std::min<int64_t>(tiles, PROJ_GRID_MAX);
     return launch(c, c->f_proj[dim_index(c->desc.dim)][up ? 0 : 1], (unsigned)grid, a, s);
 }
 

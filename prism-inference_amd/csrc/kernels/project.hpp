@@ -8,9 +8,11 @@
  * token rows are one contiguous block in and one out (HWC): they pass through
  * an LDS tile as whole rows, 16 bytes per lane, and the B fragments (token
  * 16t + l16, channels 32ks + 8g .. +7) are read from there. Workgroup = 4
- * waves; wave w computes output rows [w*OUT/4, +OUT/4) of the tile's 64
- * tokens, accumulators starting at the bias. The tile's row loads and the
- * wave's weight fragments all go out before the first MFMA.
+ * waves; wave w computes output rows [w*OUT/4, +OUT/4) of a tile's 64
+ * tokens, accumulators starting at the bias. Persistent: workgroup b takes
+ * tiles b, b + G, b + 2G, ... (G = the grid), holds its waves' weight
+ * fragments in registers across them, and requests the next tile's rows
+ * before the current tile's MFMAs.
  */
 #pragma once
 #include "common.hpp"
@@ -19,75 +21,92 @@ template <int IN, int OUT, bool RELU>
 __device__ __forceinline__ void project_body(const ProjArgs& a) {
     constexpr int KS = IN / 32;  /* k-steps                     */
     constexpr int RT = OUT / 64; /* 16-row output tiles per wave */
-    constexpr int TT = 4;        /* 16-token tiles per workgroup */
+    constexpr int TT = 4;        /* 16-token tiles per token tile */
     constexpr int LI = IN + 8, LO = OUT + 8;  /* padded LDS rows (halfs) */
     constexpr int EI = 64 * IN / 8 / 256;     /* 16-byte input chunks per thread  */
     constexpr int EO = 64 * OUT / 8 / 256;    /* 16-byte output chunks per thread */
     static_assert(IN % 32 == 0 && OUT % 64 == 0 && EI >= 1 && EO >= 1, "shape");
-    __shared__ __attribute__((aligned(16))) f16 tile[64 * (LI > LO ? LI : LO)];
+    __shared__ __attribute__((aligned(16))) f16 tin[64 * LI];
+    __shared__ __attribute__((aligned(16))) f16 tout[64 * LO];
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
-    const int64_t tok0 = (int64_t)blockIdx.x * 64;
-    const int rows = (int)min<int64_t>(64, a.n_tokens - tok0);
+    const int64_t ntiles = (a.n_tokens + 63) / 64;
 
-    /* the tile's rows are one contiguous block: 16 bytes per lane, whole
-     * cache lines per wave load; then this wave's weight fragments */
-    h8 xin[EI];
+    /* the rows of token tile `tile` (one contiguous block): 16 bytes per
+     * lane, whole cache lines per wave load; rows past the end read as zero */
+    auto load_rows = [&](int64_t tile, h8 (&x)[EI]) {
+        const int64_t tok0 = tile * 64;
+        const int rows = (int)min<int64_t>(64, a.n_tokens - tok0);
 #pragma unroll
-    for (int k = 0; k < EI; ++k) {
-        const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
-        xin[k] = r < rows ? *reinterpret_cast<const h8*>(a.in + (tok0 + r) * IN + c8) : h8{};
-    }
+        for (int k = 0; k < EI; ++k) {
+            const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
+            x[k] = r < rows ? *reinterpret_cast<const h8*>(a.in + (tok0 + r) * IN + c8) : h8{};
+        }
+    };
+    int64_t tile = blockIdx.x;
+    h8 xin[EI];
+    if (tile < ntiles) load_rows(tile, xin);
+    /* this wave's weight fragments and its bias, held for every tile */
     const FragSrc src(a.w, (unsigned)(OUT * IN * 2));
     h8 wf[RT][KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int r = 0; r < RT; ++r) wf[r][ks] = src.load((wave * RT + r) * KS + ks, lane * 16);
-#pragma unroll
-    for (int k = 0; k < EI; ++k) {
-        const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
-        *reinterpret_cast<h8*>(tile + r * LI + c8) = xin[k];
-    }
-    __syncthreads();
-
-    f4 acc[RT][TT]; /* starts at the bias */
+    f4 bias[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const int ch = (wave * RT + r) * 16 + 4 * g;
-        const f4 bb = {a.b[ch], a.b[ch + 1], a.b[ch + 2], a.b[ch + 3]};
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+        bias[r] = f4{a.b[ch], a.b[ch + 1], a.b[ch + 2], a.b[ch + 3]};
     }
+
+    for (; tile < ntiles; tile += gridDim.x) { /* uniform over the workgroup */
+        const int64_t tok0 = tile * 64;
+        const int rows = (int)min<int64_t>(64, a.n_tokens - tok0);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            const h8 xf = *reinterpret_cast<const h8*>(tile + (16 * t + l16) * LI + 32 * ks + 8 * g);
-#pragma unroll
-            for (int r = 0; r < RT; ++r) acc[r][t] = mfma_16x16x32(wf[r][ks], xf, acc[r][t]);
+        for (int k = 0; k < EI; ++k) {
+            const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
+            *reinterpret_cast<h8*>(tin + r * LI + c8) = xin[k];
         }
-    __syncthreads(); /* every wave has read the input tile */
+        __syncthreads(); /* the input tile is in; the previous tile's output rows are out of tout */
+        /* the next tile's rows go out now and arrive under this tile's MFMAs */
+        if (tile + gridDim.x < ntiles) load_rows(tile + gridDim.x, xin);
+
+        f4 acc[RT][TT]; /* starts at the bias */
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+        for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            f4 v = acc[r][t];
-            /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
-            if constexpr (RELU) {
+            for (int t = 0; t < TT; ++t) acc[r][t] = bias[r];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const h8 xf = *reinterpret_cast<const h8*>(tin + (16 * t + l16) * LI + 32 * ks + 8 * g);
+#pragma unroll
+                for (int r = 0; r < RT; ++r) acc[r][t] = mfma_16x16x32(wf[r][ks], xf, acc[r][t]);
             }
-            *reinterpret_cast<h4*>(tile + (16 * t + l16) * LO + (wave * RT + r) * 16 + 4 * g) = cvt_h4(v);
-        }
-    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < EO; ++k) {
-        const int q = threadIdx.x + 256 * k, r = q / (OUT / 8), c8 = (q % (OUT / 8)) * 8;
-        if (r < rows) *reinterpret_cast<h8*>(a.out + (tok0 + r) * OUT + c8) = *reinterpret_cast<const h8*>(tile + r * LO + c8);
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                f4 v = acc[r][t];
+                /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+                if constexpr (RELU) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+                }
+                *reinterpret_cast<h4*>(tout + (16 * t + l16) * LO + (wave * RT + r) * 16 + 4 * g) = cvt_h4(v);
+            }
+        __syncthreads(); /* the output tile is complete; every wave is done reading tin */
+#pragma unroll
+        for (int k = 0; k < EO; ++k) {
+            const int q = threadIdx.x + 256 * k, r = q / (OUT / 8), c8 = (q % (OUT / 8)) * 8;
+            if (r < rows)
+                *reinterpret_cast<h8*>(a.out + (tok0 + r) * OUT + c8) = *reinterpret_cast<const h8*>(tout + r * LO + c8);
+        }
     }
 }
 
