@@ -130,7 +130,7 @@ typedef struct CodecArgs {
 #define CODEC_TT_ENC2 2
 #define CODEC_TT_ENC3 2
 #define CODEC_TT_DEC3 2
-#define CODEC_TT_DEC2 3
+#define CODEC_TT_DEC2 4
 #define CODEC_TT_DEC1 2
 #define CODEC_RS_ENC1 1
 #define CODEC_RS_ENC2 1
