@@ -38,8 +38,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 size_t round256(size_t n) { return (n + 255) & ~size_t(255); }
 
-int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip, uint16_t* out, int batch,
-                 hipStream_t s) {
+/* The kernel arguments of stage st. */
+CodecArgs stage_args(const prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip, uint16_t* out) {
     CodecArgs a;
     memset(&a, 0, sizeof a);
     const int ir = kInRes[st], orr = kOutRes[st];
@@ -58,6 +58,13 @@ int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip,
     a.in_frame = in_pix * kInCh[st];
     a.skip_frame = out_pix * kSkipCh[st];
     a.out_frame = out_pix * kOutCh[st];
+    return a;
+}
+
+int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip, uint16_t* out, int batch,
+                 hipStream_t s) {
+    CodecArgs a = stage_args(c, st, in, skip, out);
+    const int64_t out_pix = (int64_t)a.out_w * a.out_h;
     const int64_t per_wg = 64 * kTT[st] / (kRS[st] * kKSP[st]); /* pixels per workgroup */
     const unsigned gx = st == ST_ENC0 ? (unsigned)(((a.out_w + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS) *
                                                   ((a.out_h + CODEC_ENC0_ROWS - 1) / CODEC_ENC0_ROWS))
@@ -65,6 +72,20 @@ int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip,
     void* params[] = {&a};
     const hipError_t e = hipModuleLaunchKernel(c->f_codec[st], gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(codec stage %d): %s", st, hipGetErrorString(e));
+    return PRISM_OK;
+}
+
+/* dec2 and dec1_out as one launch (prism_codec_dec21_out): 2 x 32 blocks of
+ * the r1 map, each with the 4 x 64 r0 block above it. d2 = the dec3 map, e1
+ * and e0 the skips. */
+int launch_dec21(prism_ctx* c, const uint16_t* d3, const uint16_t* e1, const uint16_t* e0, uint16_t* display,
+                 int batch, hipStream_t s) {
+    CodecArgs a2 = stage_args(c, ST_DEC2, d3, e1, nullptr);
+    CodecArgs a1 = stage_args(c, ST_DEC1, nullptr, e0, display);
+    const unsigned gx = (unsigned)(((a2.out_w + 31) / 32) * ((a2.out_h + 1) / 2));
+    void* params[] = {&a2, &a1};
+    const hipError_t e = hipModuleLaunchKernel(c->f_codec21, gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(dec2 + dec1): %s", hipGetErrorString(e));
     return PRISM_OK;
 }
 
@@ -102,7 +123,7 @@ void codec_release(prism_ctx* c) {
         c->cw[i] = nullptr;
         c->cb[i] = nullptr;
     }
-    c->ce0 = c->ce1 = c->ce2 = c->cbott = c->cchain = c->cd3 = c->cd2 = nullptr;
+    c->ce0 = c->ce1 = c->ce2 = c->cbott = c->cchain = c->cd3 = nullptr;
 }
 
 int64_t codec_frame_elems(const prism_ctx* c) { return 9LL * c->cr_w[0] * c->cr_h[0]; }
@@ -116,9 +137,11 @@ int codec_ensure_workspace(prism_ctx* c, int batch) {
     c->cws_batch = 0;
     const int64_t p0 = (int64_t)c->cr_w[0] * c->cr_h[0], p1 = (int64_t)c->cr_w[1] * c->cr_h[1];
     const int64_t p2 = (int64_t)c->cr_w[2] * c->cr_h[2], p3 = (int64_t)c->cr_w[3] * c->cr_h[3];
-    const int64_t elems[7] = {p0 * 32, p1 * 64, p2 * 128, p3 * 128, p3 * 128, p2 * 128, p1 * 64};
-    size_t off[7], total = 0;
-    for (int i = 0; i < 7; ++i) {
+    /* e0, e1, e2, bottleneck, chain output, d3 (the dec2 map stays in the
+     * fused dec2 + dec1 launch's LDS) */
+    const int64_t elems[6] = {p0 * 32, p1 * 64, p2 * 128, p3 * 128, p3 * 128, p2 * 128};
+    size_t off[6], total = 0;
+    for (int i = 0; i < 6; ++i) {
         off[i] = total;
         total += round256((size_t)batch * elems[i] * 2);
     }
@@ -135,7 +158,6 @@ int codec_ensure_workspace(prism_ctx* c, int batch) {
     c->cbott = reinterpret_cast<uint16_t*>(b + off[3]);
     c->cchain = reinterpret_cast<uint16_t*>(b + off[4]);
     c->cd3 = reinterpret_cast<uint16_t*>(b + off[5]);
-    c->cd2 = reinterpret_cast<uint16_t*>(b + off[6]);
     return PRISM_OK;
 }
 
@@ -149,8 +171,7 @@ int codec_enqueue_encode(prism_ctx* c, const uint16_t* frame, uint16_t* bottlene
 
 int codec_enqueue_decode(prism_ctx* c, const uint16_t* bottleneck, uint16_t* display, int batch, hipStream_t s) {
     int rc = launch_stage(c, ST_DEC3, bottleneck, c->ce2, c->cd3, batch, s);
-    if (!rc) rc = launch_stage(c, ST_DEC2, c->cd3, c->ce1, c->cd2, batch, s);
-    if (!rc) rc = launch_stage(c, ST_DEC1, c->cd2, c->ce0, display, batch, s);
+    if (!rc) rc = launch_dec21(c, c->cd3, c->ce1, c->ce0, display, batch, s);
     return rc;
 }
 

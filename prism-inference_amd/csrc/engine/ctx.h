@@ -92,6 +92,7 @@ struct prism_ctx {
     hipFunction_t f_take = nullptr;
     hipFunction_t f_proj[2][2] = {};    /* [dim][up, down] */
     hipFunction_t f_codec[7] = {};     /* enc0..enc3, dec3, dec2, dec1_out */
+    hipFunction_t f_codec21 = nullptr; /* dec2 + dec1_out in one launch (the decoder's last two stages) */
     std::string err;
 
     bool loaded = false;
@@ -143,7 +144,7 @@ struct prism_ctx {
     int cws_batch = 0;
     uint16_t *ce0 = nullptr, *ce1 = nullptr, *ce2 = nullptr; /* encoder maps kept for the decoder's skips */
     uint16_t *cbott = nullptr, *cchain = nullptr;             /* bottleneck in / chain out (e2e) */
-    uint16_t *cd3 = nullptr, *cd2 = nullptr;
+    uint16_t *cd3 = nullptr;
 };
 
 /* The allocation-free forward's workspace: one device array of this many

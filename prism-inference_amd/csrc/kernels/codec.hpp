@@ -328,20 +328,12 @@ __device__ __forceinline__ void codec_stage_any(const CodecArgs& a, const Src& s
     else codec_stage<Src, COUT, TT, RS, BAND>(a, src);
 }
 
-/* dec1 + output conv + PixelShuffle(2) + sigmoid. */
+/* dec1's output tiles (acc: its 32 channels, bias in) -> ReLU, fp16, the
+ * 32 -> 12 conv, fp16, sigmoid, fp16, PixelShuffle(2) into the CHW display. */
 template <int TT>
-__device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
-    const int lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l16 = lane & 15, g = lane >> 4;
-    CodecPix px[TT];
-    codec_pixels<TT, 1, false>(a, wave, l16, px);
+__device__ __forceinline__ void codec_out_shuffle(const CodecArgs& a, const CodecPix (&px)[TT], const f4 (&acc)[2][TT],
+                                                  int g, int lane) {
     const int f = blockIdx.y;
-    const SrcDec<64, 32> src{MapSrc(a.in + (int64_t)f * a.in_frame, (uint32_t)(a.in_frame * 2)),
-                             MapSrc(a.skip + (int64_t)f * a.skip_frame, (uint32_t)(a.skip_frame * 2)), a.in_w, a.in_h,
-                             a.out_w};
-    f4 acc[2][TT];
-    codec_gemm<SrcDec<64, 32>, 2, 2, TT>(src, a.w, a.b, px, g, lane, 0, acc);
     /* the 32 -> 12 weights: one fragment (rows 12..15 zero), columns permuted */
     const h8 wo = FragSrc(a.w2, 1024u).load(0, lane * 16);
     const f4 bo = {a.b2[4 * g], a.b2[4 * g + 1], a.b2[4 * g + 2], a.b2[4 * g + 3]};
@@ -374,6 +366,108 @@ __device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
         *reinterpret_cast<uint32_t*>(base) = top;
         *reinterpret_cast<uint32_t*>(base + dw) = bot;
     }
+}
+
+/* dec1 + output conv + PixelShuffle(2) + sigmoid. */
+template <int TT>
+__device__ __forceinline__ void codec_dec_out(const CodecArgs& a) {
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    CodecPix px[TT];
+    codec_pixels<TT, 1, false>(a, wave, l16, px);
+    const int f = blockIdx.y;
+    const SrcDec<64, 32> src{MapSrc(a.in + (int64_t)f * a.in_frame, (uint32_t)(a.in_frame * 2)),
+                             MapSrc(a.skip + (int64_t)f * a.skip_frame, (uint32_t)(a.skip_frame * 2)), a.in_w, a.in_h,
+                             a.out_w};
+    f4 acc[2][TT];
+    codec_gemm<SrcDec<64, 32>, 2, 2, TT>(src, a.w, a.b, px, g, lane, 0, acc);
+    codec_out_shuffle<TT>(a, px, acc, g, lane);
+}
+
+/* Decoder input read by the fused dec2 + dec1 kernel: channels [0, 64) from
+ * the workgroup's LDS block of the dec2 output (the NN-upsampled coarse map:
+ * r1 pixel (y/2, x/2), relative to the block's origin (y1, x1); LDS rows of
+ * LD halfs), [64, 96) from the e0 skip map at the same pixel. */
+struct SrcDecLds {
+    static constexpr int KS = 3, CUP = 64, CSKIP = 32, LD = 64 + 8, C1 = 32;
+    const f16* lds;
+    MapSrc ms;
+    int ow, y1, x1;
+    struct Pix {
+        uint32_t up, skip;
+    };
+    __device__ __forceinline__ Pix prep(const CodecPix& p, int g) const {
+        /* an invalid pixel reads the block's first row: in LDS, never used */
+        const int loc = p.valid ? ((p.y >> 1) - y1) * C1 + ((p.x >> 1) - x1) : 0;
+        return Pix{(uint32_t)((loc * LD + 8 * g) * 2),
+                   p.valid ? (uint32_t)(((p.y * ow + p.x) * CSKIP + 8 * g) * 2) : CODEC_OOB};
+    }
+    template <int KSP>
+    __device__ __forceinline__ h8 load(int i, int j, const Pix& q) const {
+        static_assert(KSP == 1, "no K-split");
+        if (32 * i < CUP)
+            return *reinterpret_cast<const h8*>(reinterpret_cast<const unsigned char*>(lds) + q.up + 64 * i);
+        return ms.load(q.skip + (uint32_t)(64 * i - 2 * CUP));
+    }
+};
+
+/* dec2 + dec1 + output conv + PixelShuffle(2) + sigmoid in one launch. Both
+ * decoder stages are pointwise after a nearest-neighbour upsample, so an
+ * r0 block of 4 x 64 pixels needs exactly the r1 block of 2 x 32 pixels
+ * under it: the workgroup computes that dec2 block (wave w: r1 row w/2,
+ * columns 16(w%2)..+15, all 64 channels; the same fragments, k order,
+ * rounding and ReLU as prism_codec_dec2) into LDS, then dec1 and the output
+ * for its r0 block (wave w: r0 row w, 4 tiles of 16 columns) with the
+ * upsampled channels read from LDS. The dec2 map never reaches memory; the
+ * output equals the two separate launches bit for bit. Grid: x =
+ * ceil(w1/32) * ceil(h1/2) blocks, y = frames. a2: dec2's arguments (in =
+ * the dec3 map, skip = e1, out unused); a1: dec1's (in unused, skip = e0,
+ * out = the display). */
+__device__ __forceinline__ void codec_dec21_out(const CodecArgs& a2, const CodecArgs& a1) {
+    constexpr int C1 = SrcDecLds::C1, LD = SrcDecLds::LD;
+    __shared__ __attribute__((aligned(16))) f16 d2s[2 * C1 * LD];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int f = blockIdx.y;
+    const int w1 = a2.out_w, h1 = a2.out_h, bxn = (w1 + C1 - 1) / C1;
+    const int y1 = (blockIdx.x / bxn) * 2, x1 = (blockIdx.x % bxn) * C1;
+    /* ---- dec2 for the r1 block, into LDS */
+    {
+        CodecPix px[1];
+        px[0].y = y1 + (wave >> 1);
+        px[0].x = x1 + 16 * (wave & 1) + l16;
+        px[0].valid = px[0].y < h1 && px[0].x < w1;
+        const SrcDec<128, 64> src{MapSrc(a2.in + (int64_t)f * a2.in_frame, (uint32_t)(a2.in_frame * 2)),
+                                  MapSrc(a2.skip + (int64_t)f * a2.skip_frame, (uint32_t)(a2.skip_frame * 2)),
+                                  a2.in_w, a2.in_h, w1};
+        f4 acc[4][1];
+        codec_gemm<SrcDec<128, 64>, 4, 4, 1>(src, a2.w, a2.b, px, g, lane, 0, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            f4 v = acc[r][0];
+            /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(d2s + (16 * wave + l16) * LD + 16 * r + 4 * g) = cvt_h4(v);
+        }
+    }
+    __syncthreads();
+    /* ---- dec1 + output for the r0 block */
+    constexpr int TT = 4;
+    CodecPix px[TT];
+    const int w0 = a1.out_w, h0 = a1.out_h;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        px[t].y = 2 * y1 + wave;
+        px[t].x = 2 * x1 + 16 * t + l16;
+        px[t].valid = px[t].y < h0 && px[t].x < w0;
+    }
+    const SrcDecLds src{d2s, MapSrc(a1.skip + (int64_t)f * a1.skip_frame, (uint32_t)(a1.skip_frame * 2)), w0, y1, x1};
+    f4 acc[2][TT];
+    codec_gemm<SrcDecLds, 2, 2, TT>(src, a1.w, a1.b, px, g, lane, 0, acc);
+    codec_out_shuffle<TT>(a1, px, acc, g, lane);
 }
 
 /* enc0: conv3x3 9 -> 32 + ReLU straight from the CHW frame. A workgroup
@@ -477,6 +571,9 @@ extern "C" __global__ void __launch_bounds__(256) prism_codec_dec2(CodecArgs a) 
         a, SrcDec<128, 64>{CODEC_IN_MAP, CODEC_SKIP_MAP, a.in_w, a.in_h, a.out_w});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_dec1_out(CodecArgs a) { codec_dec_out<CODEC_TT_DEC1>(a); }
+extern "C" __global__ void __launch_bounds__(256) prism_codec_dec21_out(CodecArgs a2, CodecArgs a1) {
+    codec_dec21_out(a2, a1);
+}
 #undef CODEC_FRAME
 #undef CODEC_IN_MAP
 #undef CODEC_SKIP_MAP
