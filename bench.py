@@ -177,16 +177,21 @@ def expert_kernel(d, tokens, n_experts):
 
 def measured_traffic(kernel, grid):
     """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (calibrated against a device copy of known size), if it covers this
-    kernel at this grid; None otherwise."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_moe64_b16.txt")
-    if not os.path.exists(path):
+    summaries (profiles/traffic_*_moe64_b16.txt, calibrated against a device
+    copy of known size), if one covers this kernel at this grid; None
+    otherwise."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
         return None, None
-    for line in open(path):
-        if line.startswith("bench_traffic "):
-            kv = dict(item.split("=", 1) for item in line.split()[1:])
-            if kv.get("kernel") == kernel and int(kv.get("grid", -1)) == grid:
-                return int(kv["traffic_bytes"]), os.path.relpath(path, ROOT)
+    for name in sorted(os.listdir(pdir)):
+        if not (name.startswith("traffic_") and name.endswith("_moe64_b16.txt")):
+            continue
+        path = os.path.join(pdir, name)
+        for line in open(path):
+            if line.startswith("bench_traffic "):
+                kv = dict(item.split("=", 1) for item in line.split()[1:])
+                if kv.get("kernel") == kernel and int(kv.get("grid", -1)) == grid:
+                    return int(kv["traffic_bytes"]), os.path.relpath(path, ROOT)
     return None, None
 
 
