@@ -376,7 +376,9 @@ int prism_encode(prism_ctx* ctx, const void* frame, void* bottleneck, int32_t ba
 
 /* The decoder: bottleneck fp16 [batch][r3 tokens][128] -> display fp16 CHW
  * [batch][3][2 render_h][2 render_w], with the skips of the last
- * prism_encode (same batch). */
+ * prism_encode (same batch). Two launches: dec3, then dec2 + dec1 + output
+ * conv + PixelShuffle + sigmoid in one (the dec2 map stays on chip); the
+ * result equals stages 4, 5 and 6 of prism_codec_stage bit for bit. */
 int prism_decode(prism_ctx* ctx, const void* bottleneck, void* display, int32_t batch, void* stream);
 
 /* One codec stage on caller buffers, for stage-level checks: stage 0..3 =
