@@ -161,9 +161,20 @@ int codec_ensure_workspace(prism_ctx* c, int batch) {
     return PRISM_OK;
 }
 
+/* enc0 and enc1 as one launch (prism_codec_enc01): 4 x 32 blocks of the r1
+ * map, each with the e0 region under it; writes both maps. */
+int launch_enc01(prism_ctx* c, const uint16_t* frame, uint16_t* e0, uint16_t* e1, int batch, hipStream_t s) {
+    CodecArgs a0 = stage_args(c, ST_ENC0, frame, nullptr, e0);
+    CodecArgs a1 = stage_args(c, ST_ENC1, nullptr, nullptr, e1);
+    const unsigned gx = (unsigned)(((a1.out_w + 31) / 32) * ((a1.out_h + 3) / 4));
+    void* params[] = {&a0, &a1};
+    const hipError_t e = hipModuleLaunchKernel(c->f_enc01, gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(enc0 + enc1): %s", hipGetErrorString(e));
+    return PRISM_OK;
+}
+
 int codec_enqueue_encode(prism_ctx* c, const uint16_t* frame, uint16_t* bottleneck, int batch, hipStream_t s) {
-    int rc = launch_stage(c, ST_ENC0, frame, nullptr, c->ce0, batch, s);
-    if (!rc) rc = launch_stage(c, ST_ENC1, c->ce0, nullptr, c->ce1, batch, s);
+    int rc = launch_enc01(c, frame, c->ce0, c->ce1, batch, s);
     if (!rc) rc = launch_stage(c, ST_ENC2, c->ce1, nullptr, c->ce2, batch, s);
     if (!rc) rc = launch_stage(c, ST_ENC3, c->ce2, nullptr, bottleneck, batch, s);
     return rc;

@@ -548,11 +548,169 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
     }
 }
 
+/* enc1's input taps read from the fused encoder's LDS copy of its e0 region
+ * (9 rows x 65 columns from e0 pixel (2 y1 - 1, 2 x1 - 1), LDE halfs a
+ * pixel, zeros where the region leaves the map): output pixel (y, x) of the
+ * r1 block at (y1, x1) and tap (ky, kx) read region pixel
+ * (2 (y - y1) + ky, 2 (x - x1) + kx). */
+struct SrcE0Lds {
+    static constexpr int KS = 9, EC = 65, LDE = 40;
+    const f16* lds;
+    int y1, x1;
+    struct Pix {
+        uint32_t off[9];
+    };
+    __device__ __forceinline__ Pix prep(const CodecPix& p, int g) const {
+        Pix q;
+        const int r0 = 2 * (p.y - y1), c0 = 2 * (p.x - x1); /* in the block even for pixels past the map */
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+            q.off[tap] = (uint32_t)((((r0 + tap / 3) * EC + c0 + tap % 3) * LDE + 8 * g) * 2);
+        return q;
+    }
+    template <int KSP>
+    __device__ __forceinline__ h8 load(int i, int j, const Pix& q) const {
+        static_assert(KSP == 1, "no K-split");
+        return *reinterpret_cast<const h8*>(reinterpret_cast<const unsigned char*>(lds) + q.off[i]);
+    }
+};
+
+/* enc0 + enc1 in one launch (prism_encode and the end-to-end frame; the stage
+ * calls keep them apart). A workgroup takes a 4 x 32 block of enc1 outputs at
+ * r1 (y1, x1). Its stride-2 taps need e0 rows 2 y1 - 1 .. 2 y1 + 7 and
+ * columns 2 x1 - 1 .. 2 x1 + 63, a 9 x 65 region: the workgroup copies the
+ * frame under it (11 x 67 pixels, 16 halfs each as in enc0) into LDS,
+ * computes enc0 for the region (the same fragments, tap order, rounding and
+ * ReLU as prism_codec_enc0; region pixels 16 to a tile in row-major order,
+ * one halo row and column recomputed by the neighbours) into a second LDS
+ * array, writes its own 8 x 64 e0 pixels to the e0 map (the decoder's skip),
+ * and runs enc1 with its B fragments read from that array (as
+ * prism_codec_enc1: k = tap * 32 + ic, the same fragments and order).
+ * Outputs equal the two separate launches bit for bit. Grid: x =
+ * ceil(w1/32) * ceil(h1/4) blocks in XCD bands, y = frames. a0, a1: enc0's
+ * and enc1's arguments (a1.in unused). */
+__device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs& a1) {
+    constexpr int CH = 9, CP = 16, KS0 = 5;
+    constexpr int ER = 9, EC = SrcE0Lds::EC, LDE = SrcE0Lds::LDE; /* the e0 region */
+    constexpr int FR = ER + 2, FC = EC + 2;                        /* the frame window */
+    constexpr int NREG = ER * EC, NT0 = (NREG + 15) / 16;          /* region pixels, their tiles */
+    constexpr int LDO = 64 + 8;                                    /* e1 staging row (halfs) */
+    __shared__ __attribute__((aligned(16))) f16 s_in[FR * FC * CP]; /* frame window, then e1 staging */
+    __shared__ __attribute__((aligned(16))) f16 e0s[NREG * LDE];
+    static_assert(FR * FC * CP >= 128 * LDO, "the e1 tile fits where the frame window was");
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int W0 = a0.out_w, H0 = a0.out_h, W1 = a1.out_w, H1 = a1.out_h;
+    const int bxn = (W1 + 31) / 32;
+    const int blk = codec_block<true>();
+    const int y1 = (blk / bxn) * 4, x1 = (blk % bxn) * 32; /* r1 block origin */
+    const int ey0 = 2 * y1 - 1, ex0 = 2 * x1 - 1;          /* e0 region origin */
+    /* ---- the frame window (origin ey0 - 1, ex0 - 1), 16 halfs a pixel */
+    {
+        const f16* frame = reinterpret_cast<const f16*>(a0.in) + (int64_t)blockIdx.y * a0.in_frame;
+        const int64_t plane = (int64_t)W0 * H0;
+        for (int px = threadIdx.x; px < FR * FC; px += 256) {
+            const int r = px / FC, x = px - r * FC;
+            const int gy = ey0 - 1 + r, gx = ex0 - 1 + x;
+            const bool ok = gy >= 0 && gy < H0 && gx >= 0 && gx < W0;
+            const f16* src = frame + (ok ? (int64_t)gy * W0 + gx : 0);
+            h8 lo, hi = {};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) lo[c] = ok ? src[c * plane] : (f16)0.f;
+            hi[0] = ok ? src[8 * plane] : (f16)0.f;
+            *reinterpret_cast<h8*>(s_in + px * CP) = lo;
+            *reinterpret_cast<h8*>(s_in + px * CP + 8) = hi;
+        }
+    }
+    __syncthreads();
+    /* ---- enc0 for the region; wave w takes region tiles w, w + 4, ... */
+    {
+        const FragSrc wsrc(a0.w, 2u * KS0 * 1024u);
+        h8 wf[2][KS0];
+#pragma unroll
+        for (int ks = 0; ks < KS0; ++ks) {
+            wf[0][ks] = wsrc.load(0 * KS0 + ks, lane * 16);
+            wf[1][ks] = wsrc.load(1 * KS0 + ks, lane * 16);
+        }
+        f4 bias[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int ch = 16 * r + 4 * g;
+            bias[r] = f4{a0.b[ch], a0.b[ch + 1], a0.b[ch + 2], a0.b[ch + 3]};
+        }
+        uint16_t* e0map = a0.out + (int64_t)blockIdx.y * a0.out_frame;
+        for (int tile = wave; tile < NT0; tile += 4) { /* uniform over the wave */
+            const int p = min(16 * tile + l16, NREG - 1); /* past the region: a copy of its last pixel */
+            const int er = p / EC, ec = p - er * EC;
+            f4 acc[2] = {bias[0], bias[1]};
+#pragma unroll
+            for (int ks = 0; ks < KS0; ++ks) {
+                /* k = 32 ks + 8 g + j = tap * 16 + 8 (g & 1) + j; tap 9 is padding (zero) */
+                const int tap = 2 * ks + (g >> 1), tc = tap < CH ? tap : CH - 1;
+                const int ky = tc / 3, kx = tc - 3 * ky;
+                h8 b = *reinterpret_cast<const h8*>(s_in + ((er + ky) * FC + ec + kx) * CP + 8 * (g & 1));
+                if (tap >= CH) b = h8{};
+                acc[0] = mfma_16x16x32(wf[0][ks], b, acc[0]);
+                acc[1] = mfma_16x16x32(wf[1][ks], b, acc[1]);
+            }
+            const int gy = ey0 + er, gx = ex0 + ec;
+            const bool inmap = gy >= 0 && gy < H0 && gx >= 0 && gx < W0;
+            const bool mine = inmap && er >= 1 && ec >= 1 && 16 * tile + l16 < NREG; /* this block's e0 pixels */
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                f4 v = acc[r];
+                /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+                const h4 hv = cvt_h4(v);
+                /* enc1's zero padding where the region leaves the map */
+                *reinterpret_cast<h4*>(e0s + p * LDE + 16 * r + 4 * g) = inmap ? hv : h4{};
+                if (mine) *reinterpret_cast<h4*>(e0map + ((int64_t)gy * W0 + gx) * 32 + 16 * r + 4 * g) = hv;
+            }
+        }
+    }
+    __syncthreads();
+    /* ---- enc1 for the block: wave w takes r1 row y1 + w, 2 tiles of 16 columns */
+    CodecPix px[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        px[t].y = y1 + wave;
+        px[t].x = x1 + 16 * t + l16;
+        px[t].valid = px[t].y < H1 && px[t].x < W1;
+    }
+    const SrcE0Lds src{e0s, y1, x1};
+    f4 acc[4][2];
+    codec_gemm<SrcE0Lds, 4, 4, 2>(src, a1.w, a1.b, px, g, lane, 0, acc);
+    f16* otile = s_in; /* the frame window is dead since the barrier above */
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            f4 v = acc[r][t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(otile + (32 * wave + 16 * t + l16) * LDO + 16 * r + 4 * g) = cvt_h4(v);
+        }
+    __syncthreads();
+    uint16_t* e1map = a1.out + (int64_t)blockIdx.y * a1.out_frame;
+    for (int q = threadIdx.x; q < 128 * 8; q += 256) { /* 16-byte chunks: 8 a pixel */
+        const int pl = q >> 3, c8 = (q & 7) * 8;
+        const int Y = y1 + (pl >> 5), X = x1 + (pl & 31);
+        if (Y < H1 && X < W1)
+            *reinterpret_cast<h8*>(e1map + ((int64_t)Y * W1 + X) * 64 + c8) =
+                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
+    }
+}
+
 #define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))
 #define CODEC_IN_MAP MapSrc(CODEC_FRAME(a.in, a.in_frame), (uint32_t)(a.in_frame * 2))
 #define CODEC_SKIP_MAP MapSrc(CODEC_FRAME(a.skip, a.skip_frame), (uint32_t)(a.skip_frame * 2))
 
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
+extern "C" __global__ void __launch_bounds__(256) prism_codec_enc01(CodecArgs a0, CodecArgs a1) {
+    codec_enc01(a0, a1);
+}
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
     codec_stage_any<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1, CODEC_KSP_ENC1, true>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
