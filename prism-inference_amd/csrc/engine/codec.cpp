@@ -161,12 +161,14 @@ int codec_ensure_workspace(prism_ctx* c, int batch) {
     return PRISM_OK;
 }
 
-/* enc0 and enc1 as one launch (prism_codec_enc01): 4 x 32 blocks of the r1
- * map, each with the e0 region under it; writes both maps. */
+/* enc0 and enc1 as one launch (prism_codec_enc01): CODEC_ENC01_ROWS x
+ * CODEC_ENC01_COLS blocks of the r1 map, each with the e0 region under it;
+ * writes both maps. */
 int launch_enc01(prism_ctx* c, const uint16_t* frame, uint16_t* e0, uint16_t* e1, int batch, hipStream_t s) {
     CodecArgs a0 = stage_args(c, ST_ENC0, frame, nullptr, e0);
     CodecArgs a1 = stage_args(c, ST_ENC1, nullptr, nullptr, e1);
-    const unsigned gx = (unsigned)(((a1.out_w + 31) / 32) * ((a1.out_h + 3) / 4));
+    const unsigned gx = (unsigned)(((a1.out_w + CODEC_ENC01_COLS - 1) / CODEC_ENC01_COLS) *
+                                   ((a1.out_h + CODEC_ENC01_ROWS - 1) / CODEC_ENC01_ROWS));
     void* params[] = {&a0, &a1};
     const hipError_t e = hipModuleLaunchKernel(c->f_enc01, gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(enc0 + enc1): %s", hipGetErrorString(e));

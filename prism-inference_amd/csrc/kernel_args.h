@@ -145,5 +145,9 @@ typedef struct CodecArgs {
 #define CODEC_KSP_ENC3 4
 #define CODEC_KSP_DEC3 1
 #define CODEC_KSP_DEC2 1
+/* the fused enc0 + enc1 launch: enc1 output block per workgroup (r1 rows x
+ * columns; its e0 region is (2 rows + 1) x (2 columns + 1)) */
+#define CODEC_ENC01_ROWS 4
+#define CODEC_ENC01_COLS 32
 
 #endif

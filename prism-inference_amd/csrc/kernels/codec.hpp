@@ -553,8 +553,9 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
  * pixel, zeros where the region leaves the map): output pixel (y, x) of the
  * r1 block at (y1, x1) and tap (ky, kx) read region pixel
  * (2 (y - y1) + ky, 2 (x - x1) + kx). */
+template <int EC_>
 struct SrcE0Lds {
-    static constexpr int KS = 9, EC = 65, LDE = 40;
+    static constexpr int KS = 9, EC = EC_, LDE = 40;
     const f16* lds;
     int y1, x1;
     struct Pix {
@@ -576,35 +577,41 @@ struct SrcE0Lds {
 };
 
 /* enc0 + enc1 in one launch (prism_encode and the end-to-end frame; the stage
- * calls keep them apart). A workgroup takes a 4 x 32 block of enc1 outputs at
- * r1 (y1, x1). Its stride-2 taps need e0 rows 2 y1 - 1 .. 2 y1 + 7 and
- * columns 2 x1 - 1 .. 2 x1 + 63, a 9 x 65 region: the workgroup copies the
- * frame under it (11 x 67 pixels, 16 halfs each as in enc0) into LDS,
+ * calls keep them apart). A workgroup takes a BR x BC block of enc1 outputs at
+ * r1 (y1, x1) (4 x 32: of 4 x 16 and 2 x 32 at 960 x 540 the fastest). Its
+ * stride-2 taps need e0 rows 2 y1 - 1 .. 2 y1 + 2 BR - 1 and columns
+ * 2 x1 - 1 .. 2 x1 + 2 BC - 1, a (2 BR + 1) x (2 BC + 1) region (9 x 65): the
+ * workgroup copies the frame under it (2 more rows and columns, 16 halfs a
+ * pixel as in enc0) into LDS,
  * computes enc0 for the region (the same fragments, tap order, rounding and
  * ReLU as prism_codec_enc0; region pixels 16 to a tile in row-major order,
  * one halo row and column recomputed by the neighbours) into a second LDS
- * array, writes its own 8 x 64 e0 pixels to the e0 map (the decoder's skip),
+ * array, writes its own 2 BR x 2 BC e0 pixels to the e0 map (the decoder's skip),
  * and runs enc1 with its B fragments read from that array (as
  * prism_codec_enc1: k = tap * 32 + ic, the same fragments and order).
  * Outputs equal the two separate launches bit for bit. Grid: x =
- * ceil(w1/32) * ceil(h1/4) blocks in XCD bands, y = frames. a0, a1: enc0's
+ * ceil(w1/BC) * ceil(h1/BR) blocks in XCD bands, y = frames. a0, a1: enc0's
  * and enc1's arguments (a1.in unused). */
+template <int BR, int BC>
 __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs& a1) {
     constexpr int CH = 9, CP = 16, KS0 = 5;
-    constexpr int ER = 9, EC = SrcE0Lds::EC, LDE = SrcE0Lds::LDE; /* the e0 region */
+    static_assert((BR == 2 || BR == 4) && BC % 16 == 0 && BR * BC % 64 == 0, "block of whole tiles per wave");
+    constexpr int NPX = BR * BC, TT = NPX / 64, TPR = BC / 16; /* block pixels, tiles per wave, tiles per row */
+    using Src = SrcE0Lds<2 * BC + 1>;
+    constexpr int ER = 2 * BR + 1, EC = Src::EC, LDE = Src::LDE; /* the e0 region */
     constexpr int FR = ER + 2, FC = EC + 2;                        /* the frame window */
     constexpr int NREG = ER * EC, NT0 = (NREG + 15) / 16;          /* region pixels, their tiles */
     constexpr int LDO = 64 + 8;                                    /* e1 staging row (halfs) */
     __shared__ __attribute__((aligned(16))) f16 s_in[FR * FC * CP]; /* frame window, then e1 staging */
     __shared__ __attribute__((aligned(16))) f16 e0s[NREG * LDE];
-    static_assert(FR * FC * CP >= 128 * LDO, "the e1 tile fits where the frame window was");
+    static_assert(FR * FC * CP >= NPX * LDO, "the e1 tile fits where the frame window was");
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int W0 = a0.out_w, H0 = a0.out_h, W1 = a1.out_w, H1 = a1.out_h;
-    const int bxn = (W1 + 31) / 32;
+    const int bxn = (W1 + BC - 1) / BC;
     const int blk = codec_block<true>();
-    const int y1 = (blk / bxn) * 4, x1 = (blk % bxn) * 32; /* r1 block origin */
+    const int y1 = (blk / bxn) * BR, x1 = (blk % bxn) * BC; /* r1 block origin */
     const int ey0 = 2 * y1 - 1, ex0 = 2 * x1 - 1;          /* e0 region origin */
     /* ---- the frame window (origin ey0 - 1, ex0 - 1), 16 halfs a pixel */
     {
@@ -671,32 +678,33 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
         }
     }
     __syncthreads();
-    /* ---- enc1 for the block: wave w takes r1 row y1 + w, 2 tiles of 16 columns */
-    CodecPix px[2];
+    /* ---- enc1 for the block: wave w takes its TT 16-pixel tiles, row-major */
+    CodecPix px[TT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        px[t].y = y1 + wave;
-        px[t].x = x1 + 16 * t + l16;
+    for (int t = 0; t < TT; ++t) {
+        const int tile = wave * TT + t;
+        px[t].y = y1 + tile / TPR;
+        px[t].x = x1 + 16 * (tile % TPR) + l16;
         px[t].valid = px[t].y < H1 && px[t].x < W1;
     }
-    const SrcE0Lds src{e0s, y1, x1};
-    f4 acc[4][2];
-    codec_gemm<SrcE0Lds, 4, 4, 2>(src, a1.w, a1.b, px, g, lane, 0, acc);
+    const Src src{e0s, y1, x1};
+    f4 acc[4][TT];
+    codec_gemm<Src, 4, 4, TT>(src, a1.w, a1.b, px, g, lane, 0, acc);
     f16* otile = s_in; /* the frame window is dead since the barrier above */
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             f4 v = acc[r][t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
-            *reinterpret_cast<h4*>(otile + (32 * wave + 16 * t + l16) * LDO + 16 * r + 4 * g) = cvt_h4(v);
+            *reinterpret_cast<h4*>(otile + (16 * (wave * TT + t) + l16) * LDO + 16 * r + 4 * g) = cvt_h4(v);
         }
     __syncthreads();
     uint16_t* e1map = a1.out + (int64_t)blockIdx.y * a1.out_frame;
-    for (int q = threadIdx.x; q < 128 * 8; q += 256) { /* 16-byte chunks: 8 a pixel */
+    for (int q = threadIdx.x; q < NPX * 8; q += 256) { /* 16-byte chunks: 8 a pixel */
         const int pl = q >> 3, c8 = (q & 7) * 8;
-        const int Y = y1 + (pl >> 5), X = x1 + (pl & 31);
+        const int Y = y1 + pl / BC, X = x1 + pl % BC;
         if (Y < H1 && X < W1)
             *reinterpret_cast<h8*>(e1map + ((int64_t)Y * W1 + X) * 64 + c8) =
                 *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
@@ -709,7 +717,7 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
 
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc01(CodecArgs a0, CodecArgs a1) {
-    codec_enc01(a0, a1);
+    codec_enc01<CODEC_ENC01_ROWS, CODEC_ENC01_COLS>(a0, a1);
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
     codec_stage_any<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1, CODEC_KSP_ENC1, true>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
