@@ -130,8 +130,10 @@ def codec_section(hip, eng, desc, steps, warmup, reps, stream):
         stages[name] = {"ms": round(ms, 5), "bytes": int(nbytes), "hbm_frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
                         "tflops": round(2 * macs * pix[ro] / (ms * 1e-3) / 1e12, 2)}
     total = sum(v["ms"] for v in stages.values())
-    # the frame's own codec launches: prism_encode (enc0..enc3) and prism_decode
-    # (dec3, then dec2 + dec1 + output in one launch, the dec2 map kept in LDS)
+    # the frame's own codec launches: prism_encode (enc0 + enc1 in one launch,
+    # enc1's taps read from the workgroup's e0 region in LDS; enc2; enc3) and
+    # prism_decode (dec3, then dec2 + dec1 + output in one launch, the dec2 map
+    # kept in LDS)
     t_enc = time_stage(hip, lambda: eng.L.prism_encode(eng.h, frame, b3, 1, stream), reps, stream)
     t_dec = time_stage(hip, lambda: eng.L.prism_decode(eng.h, b3, disp, 1, stream), reps, stream)
     for ptr in list(bufs.values()) + [frame, disp, b3]:
@@ -140,9 +142,9 @@ def codec_section(hip, eng, desc, steps, warmup, reps, stream):
             "codec_ms": round(total, 5),
             "codec_hbm_frac": round(sum(v["bytes"] for v in stages.values()) / (total * 1e-3) / HBM_PEAK, 4),
             "frame_codec_launches": {"encode_ms": round(t_enc, 5), "decode_ms": round(t_dec, 5),
-                                     "note": "prism_encode (enc0..enc3) and prism_decode (dec3, then dec2 + dec1 + "
-                                             "output conv + PixelShuffle/sigmoid in one launch), back to back; "
-                                             "codec_ms and stages are the seven stage calls"},
+                                     "note": "prism_encode (enc0 + enc1 in one launch, enc2, enc3) and prism_decode "
+                                             "(dec3, then dec2 + dec1 + output conv + PixelShuffle/sigmoid in one "
+                                             "launch), back to back; codec_ms and stages are the seven stage calls"},
             "stages": stages,
             "workload": f"render {w0}x{h0} (9-channel frame) -> encoder -> proj 128->256 -> 16 MoE-64 blocks at "
                         f"{r[3][0]}x{r[3][1]} -> proj 256->128 -> decoder -> 3x{2 * w0}x{2 * h0} display, batch 1, "
