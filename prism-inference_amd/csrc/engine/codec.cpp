@@ -68,7 +68,9 @@ int launch_stage(prism_ctx* c, int st, const uint16_t* in, const uint16_t* skip,
     const int64_t per_wg = 64 * kTT[st] / (kRS[st] * kKSP[st]); /* pixels per workgroup */
     const unsigned gx = st == ST_ENC0 ? (unsigned)(((a.out_w + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS) *
                                                   ((a.out_h + CODEC_ENC0_ROWS - 1) / CODEC_ENC0_ROWS))
-                                      : (unsigned)((out_pix + per_wg - 1) / per_wg);
+                        : st == ST_ENC2 ? (unsigned)(((a.out_w + CODEC_WIN_COLS_ENC2 - 1) / CODEC_WIN_COLS_ENC2) *
+                                                     ((a.out_h + CODEC_WIN_ROWS_ENC2 - 1) / CODEC_WIN_ROWS_ENC2))
+                                        : (unsigned)((out_pix + per_wg - 1) / per_wg);
     void* params[] = {&a};
     const hipError_t e = hipModuleLaunchKernel(c->f_codec[st], gx, (unsigned)batch, 1, 256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(codec stage %d): %s", st, hipGetErrorString(e));

@@ -149,5 +149,10 @@ typedef struct CodecArgs {
  * columns; its e0 region is (2 rows + 1) x (2 columns + 1)) */
 #define CODEC_ENC01_ROWS 4
 #define CODEC_ENC01_COLS 32
+/* enc2 over an LDS window (codec_conv_window): output block rows x columns,
+ * weight fragments this many k-steps ahead */
+#define CODEC_WIN_ROWS_ENC2 2
+#define CODEC_WIN_COLS_ENC2 16
+#define CODEC_WIN_DW_ENC2 3
 
 #endif

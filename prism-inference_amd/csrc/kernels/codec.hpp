@@ -548,6 +548,118 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
     }
 }
 
+/* A stride-2 conv3x3 stage over an LDS window (enc2): the workgroup takes a
+ * BR x BC block of output pixels and first copies the input window under it,
+ * (2 BR + 1) x (2 BC + 1) pixels of CIN channels (zeros past the map), into
+ * LDS with coalesced 16-byte loads; each wave then takes a quarter of the
+ * output channels over all BR x BC / 16 tiles of the block, its B fragments
+ * read from the window (tap (ky, kx) of output pixel (y, x) at window pixel
+ * (2 (y - oy0) + ky, 2 (x - ox0) + kx)) and its weight fragments streamed DW
+ * k-steps ahead. No input tap or weight fragment is fetched by more than
+ * one wave of the workgroup (the one-wave-per-pixel-group form fetches each
+ * weight fragment in every wave). k order and sums as codec_stage:
+ * bit-identical outputs. */
+template <int CIN, int COUT, int BR, int BC, int DW, bool BAND>
+__device__ __forceinline__ void codec_conv_window(const CodecArgs& a) {
+    constexpr int WR = 2 * BR + 1, WC = 2 * BC + 1, LDE = CIN + 8; /* window, LDS pixel stride (halfs) */
+    constexpr int NPX = BR * BC, TT = NPX / 16, TPR = BC / 16;
+    constexpr int RTALL = COUT / 16, RT = RTALL / 4, CPT = CIN / 32, KS = 9 * CPT;
+    constexpr int CPP = CIN / 8, LDO = COUT + 8;
+    static_assert(BC % 16 == 0 && RTALL % 4 == 0 && CIN % 32 == 0 && DW >= 1 && DW <= KS, "window stage shape");
+    static_assert(WR * WC * LDE >= NPX * LDO, "the output tile fits where the window was");
+    __shared__ __attribute__((aligned(16))) f16 win[WR * WC * LDE];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int iw = a.in_w, ih = a.in_h, ow = a.out_w, oh = a.out_h;
+    const int bxn = (ow + BC - 1) / BC;
+    const int blk = codec_block<BAND>();
+    const int oy0 = (blk / bxn) * BR, ox0 = (blk % bxn) * BC;
+    const int wy0 = 2 * oy0 - 1, wx0 = 2 * ox0 - 1;
+    const uint16_t* in = a.in + (int64_t)blockIdx.y * a.in_frame;
+    for (int q = threadIdx.x; q < WR * WC * CPP; q += 256) {
+        const int px = q / CPP, c8 = (q - px * CPP) * 8;
+        const int r = px / WC, c = px - r * WC;
+        const int gy = wy0 + r, gx = wx0 + c;
+        const bool ok = gy >= 0 && gy < ih && gx >= 0 && gx < iw;
+        *reinterpret_cast<h8*>(win + px * LDE + c8) =
+            ok ? *reinterpret_cast<const h8*>(in + ((int64_t)gy * iw + gx) * CIN + c8) : h8{};
+    }
+    __syncthreads();
+    const int rt0 = wave * RT;
+    f4 acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int ch = 16 * (rt0 + r) + 4 * g;
+        const f4 bb = {a.b[ch], a.b[ch + 1], a.b[ch + 2], a.b[ch + 3]};
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = bb;
+    }
+    /* this lane's window pixel for tap 0 of each tile (byte offsets) */
+    uint32_t boff[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int ly = t / TPR, lx = 16 * (t % TPR) + l16;
+        boff[t] = (uint32_t)(((2 * ly * WC + 2 * lx) * LDE + 8 * g) * 2);
+    }
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(win);
+    auto bload = [&](int ks, int t) {
+        const int tap = ks / CPT, c = ks % CPT;
+        return *reinterpret_cast<const h8*>(wb + boff[t] + (((tap / 3) * WC + tap % 3) * LDE + 32 * c) * 2);
+    };
+    const FragSrc wsrc(a.w, (unsigned)(RTALL * KS * 1024));
+    h8 wq[DW][RT];
+#pragma unroll
+    for (int d = 0; d < DW; ++d)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) wq[d][r] = wsrc.load((rt0 + r) * KS + d, lane * 16);
+    h8 bc[TT], bn[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) bc[t] = bload(0, t);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) bn[t] = bload(ks + 1, t);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wq[ks % DW][r], bc[t], acc[r][t]);
+        if (ks + DW < KS) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) wq[ks % DW][r] = wsrc.load((rt0 + r) * KS + ks + DW, lane * 16);
+        }
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) bc[t] = bn[t];
+        }
+        sched_fence();
+    }
+    __syncthreads(); /* every wave is done reading the window */
+    f16* otile = win;
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            f4 v = acc[r][t];
+            /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+            *reinterpret_cast<h4*>(otile + (16 * t + l16) * LDO + 16 * (rt0 + r) + 4 * g) = cvt_h4(v);
+        }
+    __syncthreads();
+    uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
+    constexpr int OPP = COUT / 8; /* 16-byte chunks a pixel */
+    for (int q = threadIdx.x; q < NPX * OPP; q += 256) {
+        const int pl = q / OPP, c8 = (q - pl * OPP) * 8;
+        const int y = oy0 + pl / BC, x = ox0 + pl % BC;
+        if (y < oh && x < ow)
+            *reinterpret_cast<h8*>(out + ((int64_t)y * ow + x) * COUT + c8) =
+                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
+    }
+}
+
 /* enc1's input taps read from the fused encoder's LDS copy of its e0 region
  * (9 rows x 65 columns from e0 pixel (2 y1 - 1, 2 x1 - 1), LDE halfs a
  * pixel, zeros where the region leaves the map): output pixel (y, x) of the
@@ -723,7 +835,7 @@ extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) 
     codec_stage_any<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1, CODEC_KSP_ENC1, true>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc2(CodecArgs a) {
-    codec_stage_any<SrcConvNHWC<64, 2>, 128, CODEC_TT_ENC2, CODEC_RS_ENC2, CODEC_KSP_ENC2, true>(a, SrcConvNHWC<64, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
+    codec_conv_window<64, 128, CODEC_WIN_ROWS_ENC2, CODEC_WIN_COLS_ENC2, CODEC_WIN_DW_ENC2, true>(a);
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc3(CodecArgs a) {
     codec_stage_any<SrcConvNHWC<128, 2>, 128, CODEC_TT_ENC3, CODEC_RS_ENC3, CODEC_KSP_ENC3, false>(a, SrcConvNHWC<128, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
