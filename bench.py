@@ -131,7 +131,8 @@ def codec_section(hip, eng, desc, steps, warmup, reps, stream):
                         "tflops": round(2 * macs * pix[ro] / (ms * 1e-3) / 1e12, 2)}
     total = sum(v["ms"] for v in stages.values())
     # the frame's own codec launches: prism_encode (enc0 + enc1 in one launch,
-    # enc1's taps read from the workgroup's e0 region in LDS; enc2; enc3) and
+    # enc1's taps read from the workgroup's e0 region in LDS; then enc2 + enc3
+    # in one launch, enc3's taps read from the workgroup's e2 region) and
     # prism_decode (dec3, then dec2 + dec1 + output in one launch, the dec2 map
     # kept in LDS)
     t_enc = time_stage(hip, lambda: eng.L.prism_encode(eng.h, frame, b3, 1, stream), reps, stream)
@@ -142,7 +143,7 @@ def codec_section(hip, eng, desc, steps, warmup, reps, stream):
             "codec_ms": round(total, 5),
             "codec_hbm_frac": round(sum(v["bytes"] for v in stages.values()) / (total * 1e-3) / HBM_PEAK, 4),
             "frame_codec_launches": {"encode_ms": round(t_enc, 5), "decode_ms": round(t_dec, 5),
-                                     "note": "prism_encode (enc0 + enc1 in one launch, enc2, enc3) and prism_decode "
+                                     "note": "prism_encode (enc0 + enc1 in one launch, then enc2 + enc3 in one) and prism_decode "
                                              "(dec3, then dec2 + dec1 + output conv + PixelShuffle/sigmoid in one "
                                              "launch), back to back; codec_ms and stages are the seven stage calls"},
             "stages": stages,

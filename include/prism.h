@@ -371,9 +371,10 @@ int prism_load_codec(prism_ctx* ctx, const void* blob, size_t bytes, const prism
 /* The encoder: frame fp16 CHW [batch][9][render_h][render_w] -> bottleneck
  * fp16 [batch][r3 tokens][128] (token-major, the adapted chain's input). The
  * encoder maps stay in the engine for the next prism_decode of `batch`
- * frames. Three launches: enc0 + enc1 in one (enc1 reads its input from the
- * workgroup's on-chip copy of e0), enc2, enc3; the result equals stages 0-3
- * of prism_codec_stage bit for bit. */
+ * frames. Two launches: enc0 + enc1 in one (enc1 reads its input from the
+ * workgroup's on-chip copy of e0), then enc2 + enc3 in one (enc3 reads its
+ * input from the workgroup's on-chip copy of e2); the result equals stages
+ * 0-3 of prism_codec_stage bit for bit. */
 int prism_encode(prism_ctx* ctx, const void* frame, void* bottleneck, int32_t batch, void* stream);
 
 /* The decoder: bottleneck fp16 [batch][r3 tokens][128] -> display fp16 CHW

@@ -177,10 +177,23 @@ int launch_enc01(prism_ctx* c, const uint16_t* frame, uint16_t* e0, uint16_t* e1
     return PRISM_OK;
 }
 
+/* enc2 and enc3 as one launch (prism_codec_enc23): CODEC_ENC23_ROWS x
+ * CODEC_ENC23_COLS blocks of the bottleneck, each with the e2 region and the
+ * e1 window under it; writes the e2 map and the bottleneck. 8 waves. */
+int launch_enc23(prism_ctx* c, const uint16_t* e1, uint16_t* e2, uint16_t* bottleneck, int batch, hipStream_t s) {
+    CodecArgs a2 = stage_args(c, ST_ENC2, e1, nullptr, e2);
+    CodecArgs a3 = stage_args(c, ST_ENC3, nullptr, nullptr, bottleneck);
+    const unsigned gx = (unsigned)(((a3.out_w + CODEC_ENC23_COLS - 1) / CODEC_ENC23_COLS) *
+                                   ((a3.out_h + CODEC_ENC23_ROWS - 1) / CODEC_ENC23_ROWS));
+    void* params[] = {&a2, &a3};
+    const hipError_t e = hipModuleLaunchKernel(c->f_enc23, gx, (unsigned)batch, 1, 512, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, PRISM_ERR_HIP, "hipModuleLaunchKernel(enc2 + enc3): %s", hipGetErrorString(e));
+    return PRISM_OK;
+}
+
 int codec_enqueue_encode(prism_ctx* c, const uint16_t* frame, uint16_t* bottleneck, int batch, hipStream_t s) {
     int rc = launch_enc01(c, frame, c->ce0, c->ce1, batch, s);
-    if (!rc) rc = launch_stage(c, ST_ENC2, c->ce1, nullptr, c->ce2, batch, s);
-    if (!rc) rc = launch_stage(c, ST_ENC3, c->ce2, nullptr, bottleneck, batch, s);
+    if (!rc) rc = launch_enc23(c, c->ce1, c->ce2, bottleneck, batch, s);
     return rc;
 }
 

@@ -94,6 +94,7 @@ struct prism_ctx {
     hipFunction_t f_codec[7] = {};     /* enc0..enc3, dec3, dec2, dec1_out */
     hipFunction_t f_codec21 = nullptr; /* dec2 + dec1_out in one launch (the decoder's last two stages) */
     hipFunction_t f_enc01 = nullptr;   /* enc0 + enc1 in one launch (the encoder's first two stages) */
+    hipFunction_t f_enc23 = nullptr;   /* enc2 + enc3 in one launch (the encoder's last two stages) */
     std::string err;
 
     bool loaded = false;

@@ -109,7 +109,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_codec[0], "prism_codec_enc0"}, {&c->f_codec[1], "prism_codec_enc1"},
         {&c->f_codec[2], "prism_codec_enc2"}, {&c->f_codec[3], "prism_codec_enc3"},
         {&c->f_codec[4], "prism_codec_dec3"}, {&c->f_codec[5], "prism_codec_dec2"},
-        {&c->f_codec[6], "prism_codec_dec1_out"}, {&c->f_codec21, "prism_codec_dec21_out"}, {&c->f_enc01, "prism_codec_enc01"},
+        {&c->f_codec[6], "prism_codec_dec1_out"}, {&c->f_codec21, "prism_codec_dec21_out"},
+        {&c->f_enc01, "prism_codec_enc01"},   {&c->f_enc23, "prism_codec_enc23"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);

@@ -149,6 +149,11 @@ typedef struct CodecArgs {
  * columns; its e0 region is (2 rows + 1) x (2 columns + 1)) */
 #define CODEC_ENC01_ROWS 4
 #define CODEC_ENC01_COLS 32
+/* the fused enc2 + enc3 launch: enc3 output block per workgroup (r3 rows x
+ * columns, 32 pixels), and whether the blocks go to the XCDs in bands */
+#define CODEC_ENC23_ROWS 4
+#define CODEC_ENC23_COLS 8
+#define CODEC_ENC23_BAND 1
 /* enc2 over an LDS window (codec_conv_window): output block rows x columns,
  * weight fragments this many k-steps ahead */
 #define CODEC_WIN_ROWS_ENC2 2

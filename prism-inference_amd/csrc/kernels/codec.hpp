@@ -256,21 +256,24 @@ __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) 
  * tiles of the other rows in LDS, sums the group's KSP partials of its own
  * rows in wave order (the first carries the bias), ReLU, fp16, into the
  * output tile. */
-template <class Src, int COUT, int TT, int KSP, bool BAND>
-__device__ __forceinline__ void codec_stage_ksplit(const CodecArgs& a, const Src& src) {
-    constexpr int RTALL = COUT / 16, RQ = RTALL / KSP, NO = RTALL - RQ;
-    static_assert(COUT % 16 == 0 && 4 % KSP == 0 && RTALL % KSP == 0, "K-split shape");
-    constexpr int NPX = (4 / KSP) * TT * 16, LDO = COUT + 8;
-    __shared__ __attribute__((aligned(16))) f4 part[4 * NO * TT * 64]; /* [wave][row tile not owned][t][lane] */
-    __shared__ __attribute__((aligned(16))) f16 otile[NPX * LDO];
-    const int lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l16 = lane & 15, g = lane >> 4;
+/* The K-split reduction: wave `wave`, position kq = wave % KSP of pixel
+ * group wave / KSP, holds partial sums of all RTALL row tiles over its
+ * k-steps (acc); it publishes those of the rows it does not own in `part`
+ * ([wave][row tile not owned][t][lane]), then sums the group's KSP partials
+ * of its own RQ = RTALL / KSP rows from kq RQ in wave order (the first
+ * carries the bias): ReLU, fp16, into the output tile (pixel row
+ * pg TT 16 + 16 t + l16, LDO halfs a row). One workgroup barrier, between
+ * publishing and summing. */
+template <int RTALL, int TT, int KSP, int LDO>
+__device__ __forceinline__ void codec_ksplit_reduce(const f4 (&accin)[RTALL][TT], f4* part, f16* otile, int wave,
+                                                    int lane, int l16, int g) {
+    constexpr int RQ = RTALL / KSP, NO = RTALL - RQ;
+    f4 acc[RTALL][TT]; /* a local copy: selected from below without indexing registers */
+#pragma unroll
+    for (int r = 0; r < RTALL; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = accin[r][t];
     const int pg = wave / KSP, kq = wave % KSP;
-    CodecPix px[TT];
-    codec_pixels<TT, KSP, BAND>(a, wave, l16, px);
-    f4 acc[RTALL][TT];
-    codec_gemm<Src, RTALL, RTALL, TT, KSP>(src, a.w, a.b, px, g, lane, 0, acc, kq);
     /* the slot of row tile r (not owned by position j) of wave w; for an owned
      * r (a value the reduction computes and does not use) a slot in range */
     auto slot = [&](int w, int j, int r, int t) {
@@ -308,6 +311,23 @@ __device__ __forceinline__ void codec_stage_ksplit(const CodecArgs& a, const Src
             *reinterpret_cast<h4*>(otile + (pl0 + 16 * t + l16) * LDO + 16 * r + 4 * g) = cvt_h4(v);
         }
     }
+}
+
+template <class Src, int COUT, int TT, int KSP, bool BAND>
+__device__ __forceinline__ void codec_stage_ksplit(const CodecArgs& a, const Src& src) {
+    constexpr int RTALL = COUT / 16, RQ = RTALL / KSP, NO = RTALL - RQ;
+    static_assert(COUT % 16 == 0 && 4 % KSP == 0 && RTALL % KSP == 0, "K-split shape");
+    constexpr int NPX = (4 / KSP) * TT * 16, LDO = COUT + 8;
+    __shared__ __attribute__((aligned(16))) f4 part[4 * NO * TT * 64]; /* [wave][row tile not owned][t][lane] */
+    __shared__ __attribute__((aligned(16))) f16 otile[NPX * LDO];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    CodecPix px[TT];
+    codec_pixels<TT, KSP, BAND>(a, wave, l16, px);
+    f4 acc[RTALL][TT];
+    codec_gemm<Src, RTALL, RTALL, TT, KSP>(src, a.w, a.b, px, g, lane, 0, acc, wave % KSP);
+    codec_ksplit_reduce<RTALL, TT, KSP, LDO>(acc, part, otile, wave, lane, l16, g);
     __syncthreads();
     const int64_t p0 = (int64_t)codec_block<BAND>() * NPX, npix = (int64_t)a.out_w * a.out_h;
     uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
@@ -660,31 +680,33 @@ __device__ __forceinline__ void codec_conv_window(const CodecArgs& a) {
     }
 }
 
-/* enc1's input taps read from the fused encoder's LDS copy of its e0 region
- * (9 rows x 65 columns from e0 pixel (2 y1 - 1, 2 x1 - 1), LDE halfs a
- * pixel, zeros where the region leaves the map): output pixel (y, x) of the
- * r1 block at (y1, x1) and tap (ky, kx) read region pixel
- * (2 (y - y1) + ky, 2 (x - x1) + kx). */
-template <int EC_>
-struct SrcE0Lds {
-    static constexpr int KS = 9, EC = EC_, LDE = 40;
+/* A stride-2 conv3x3's taps read from an LDS copy of the input region under
+ * an output block at (y0, x0): output pixel (y, x) and tap (ky, kx) read
+ * region pixel (2 (y - y0) + ky, 2 (x - x0) + kx), EC pixels a region row,
+ * LDE halfs a pixel, zeros where the region leaves the map; k = tap * CIN +
+ * ic as SrcConvNHWC. For pixels past the map the offsets stay in the region. */
+template <int CIN, int EC, int LDE>
+struct SrcRegionLds {
+    static constexpr int KS = 9 * CIN / 32, CPT = CIN / 32;
     const f16* lds;
-    int y1, x1;
+    int y0, x0;
     struct Pix {
         uint32_t off[9];
     };
     __device__ __forceinline__ Pix prep(const CodecPix& p, int g) const {
         Pix q;
-        const int r0 = 2 * (p.y - y1), c0 = 2 * (p.x - x1); /* in the block even for pixels past the map */
+        const int r0 = 2 * (p.y - y0), c0 = 2 * (p.x - x0);
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap)
             q.off[tap] = (uint32_t)((((r0 + tap / 3) * EC + c0 + tap % 3) * LDE + 8 * g) * 2);
         return q;
     }
+    /* k-step i KSP + j (i compile-time, j < KSP wave-uniform) */
     template <int KSP>
     __device__ __forceinline__ h8 load(int i, int j, const Pix& q) const {
-        static_assert(KSP == 1, "no K-split");
-        return *reinterpret_cast<const h8*>(reinterpret_cast<const unsigned char*>(lds) + q.off[i]);
+        static_assert(CPT % KSP == 0, "a split's k-steps stay within one tap");
+        return *reinterpret_cast<const h8*>(reinterpret_cast<const unsigned char*>(lds) + q.off[i * KSP / CPT] +
+                                            (((i * KSP) % CPT + j) * 64));
     }
 };
 
@@ -709,8 +731,8 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
     constexpr int CH = 9, CP = 16, KS0 = 5;
     static_assert((BR == 2 || BR == 4) && BC % 16 == 0 && BR * BC % 64 == 0, "block of whole tiles per wave");
     constexpr int NPX = BR * BC, TT = NPX / 64, TPR = BC / 16; /* block pixels, tiles per wave, tiles per row */
-    using Src = SrcE0Lds<2 * BC + 1>;
-    constexpr int ER = 2 * BR + 1, EC = Src::EC, LDE = Src::LDE; /* the e0 region */
+    constexpr int ER = 2 * BR + 1, EC = 2 * BC + 1, LDE = 40; /* the e0 region, 32 channels a pixel */
+    using Src = SrcRegionLds<32, EC, LDE>;
     constexpr int FR = ER + 2, FC = EC + 2;                        /* the frame window */
     constexpr int NREG = ER * EC, NT0 = (NREG + 15) / 16;          /* region pixels, their tiles */
     constexpr int LDO = 64 + 8;                                    /* e1 staging row (halfs) */
@@ -823,6 +845,160 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
     }
 }
 
+/* enc2 + enc3 in one launch (prism_encode and the end-to-end frame; the stage
+ * calls keep them apart), 8 waves. A workgroup takes a BR x BC block of enc3
+ * outputs (32 pixels) at r3 (y3, x3). enc3's stride-2 taps need e2 rows
+ * 2 y3 - 1 .. 2 y3 + 2 BR - 1 and columns 2 x3 - 1 .. 2 x3 + 2 BC - 1, a
+ * (2 BR + 1) x (2 BC + 1) region, whose own taps need a (4 BR + 3) x
+ * (4 BC + 3) window of e1. The workgroup copies that e1 window into LDS,
+ * computes enc2 for the region into a second LDS array with each wave taking
+ * one of enc2's 8 output row tiles over all the region's pixels (as
+ * prism_codec_enc2: the same fragments, k order, rounding and ReLU; zeros
+ * where the region leaves the map, which is enc3's padding), writes its own
+ * 2 BR x 2 BC e2 pixels to the e2 map (the decoder's skip) as whole pixel
+ * rows, and runs enc3 from the region as prism_codec_enc3 does: its
+ * reduction split over KSP = 4 waves (two pixel groups of one 16-pixel tile
+ * each), partials summed in wave order. Outputs equal the two separate
+ * launches bit for bit. Grid: x = ceil(w3/BC) * ceil(h3/BR) blocks, y =
+ * frames. a2, a3: enc2's and enc3's arguments (a3.in unused). */
+template <int BR, int BC, bool BAND>
+__device__ __forceinline__ void codec_enc23(const CodecArgs& a2, const CodecArgs& a3) {
+    constexpr int C1 = 64, C2 = 128, C3 = 128, NW = 8, KSP = 4;
+    constexpr int ER = 2 * BR + 1, EC = 2 * BC + 1;          /* the e2 region */
+    constexpr int WR = 2 * ER + 1, WC = 2 * EC + 1;          /* the e1 window */
+    constexpr int L1 = C1 + 8, L2 = C2 + 8, LDO = C3 + 8;    /* LDS pixel strides (halfs) */
+    constexpr int NREG = ER * EC, NT2 = (NREG + 15) / 16;    /* region pixels, their tiles */
+    constexpr int NPX = BR * BC, TT3 = 1;                    /* enc3 block: 2 groups x 1 tile */
+    constexpr int RT3 = C3 / 16, NO = RT3 - RT3 / KSP;
+    constexpr int CPT2 = C1 / 32, KS2 = 9 * CPT2, RTALL2 = C2 / 16, DW = 3;
+    static_assert(NPX == 16 * TT3 * NW / KSP && RTALL2 == NW, "8 waves: one enc2 row tile each, 2 x 4 for enc3");
+    static_assert(NW * NO * TT3 * 64 * 16 + NPX * LDO * 2 <= WR * WC * L1 * 2,
+                  "enc3's partials and output tile fit where the e1 window was");
+    __shared__ __attribute__((aligned(16))) f16 win[WR * WC * L1]; /* e1 window; then partials + e3 tile */
+    __shared__ __attribute__((aligned(16))) f16 e2s[NREG * L2];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int W1 = a2.in_w, H1 = a2.in_h, W2 = a2.out_w, H2 = a2.out_h, W3 = a3.out_w, H3 = a3.out_h;
+    const int bxn = (W3 + BC - 1) / BC;
+    const int blk = codec_block<BAND>();
+    const int y3 = (blk / bxn) * BR, x3 = (blk % bxn) * BC; /* r3 block origin */
+    const int ey0 = 2 * y3 - 1, ex0 = 2 * x3 - 1;          /* e2 region origin */
+    const int wy0 = 2 * ey0 - 1, wx0 = 2 * ex0 - 1;        /* e1 window origin */
+    /* ---- the e1 window */
+    {
+        const uint16_t* e1 = a2.in + (int64_t)blockIdx.y * a2.in_frame;
+        constexpr int CPP = C1 / 8;
+        for (int q = threadIdx.x; q < WR * WC * CPP; q += 64 * NW) {
+            const int px = q / CPP, c8 = (q - px * CPP) * 8;
+            const int r = px / WC, c = px - r * WC;
+            const int gy = wy0 + r, gx = wx0 + c;
+            const bool ok = gy >= 0 && gy < H1 && gx >= 0 && gx < W1;
+            *reinterpret_cast<h8*>(win + px * L1 + c8) =
+                ok ? *reinterpret_cast<const h8*>(e1 + ((int64_t)gy * W1 + gx) * C1 + c8) : h8{};
+        }
+    }
+    __syncthreads();
+    /* ---- enc2 for the region: wave w takes row tile w over all NT2 tiles */
+    {
+        f4 acc[NT2];
+        {
+            const int ch = 16 * wave + 4 * g;
+            const f4 bb = {a2.b[ch], a2.b[ch + 1], a2.b[ch + 2], a2.b[ch + 3]};
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) acc[t] = bb;
+        }
+        uint32_t boff[NT2]; /* this lane's window pixel for tap 0 of each tile (bytes) */
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            const int p = min(16 * t + l16, NREG - 1); /* past the region: a copy of its last pixel */
+            const int er = p / EC, ec = p - er * EC;
+            boff[t] = (uint32_t)(((2 * er * WC + 2 * ec) * L1 + 8 * g) * 2);
+        }
+        const unsigned char* wb = reinterpret_cast<const unsigned char*>(win);
+        auto bload = [&](int ks, int t) {
+            const int tap = ks / CPT2, c = ks % CPT2;
+            return *reinterpret_cast<const h8*>(wb + boff[t] + (((tap / 3) * WC + tap % 3) * L1 + 32 * c) * 2);
+        };
+        const FragSrc wsrc(a2.w, (unsigned)(RTALL2 * KS2 * 1024));
+        h8 wq[DW];
+#pragma unroll
+        for (int d = 0; d < DW; ++d) wq[d] = wsrc.load(wave * KS2 + d, lane * 16);
+        h8 bc[NT2], bn[NT2];
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) bc[t] = bload(0, t);
+#pragma unroll
+        for (int ks = 0; ks < KS2; ++ks) {
+            if (ks + 1 < KS2) {
+#pragma unroll
+                for (int t = 0; t < NT2; ++t) bn[t] = bload(ks + 1, t);
+            }
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) acc[t] = mfma_16x16x32(wq[ks % DW], bc[t], acc[t]);
+            if (ks + DW < KS2) wq[ks % DW] = wsrc.load(wave * KS2 + ks + DW, lane * 16);
+            if (ks + 1 < KS2) {
+#pragma unroll
+                for (int t = 0; t < NT2; ++t) bc[t] = bn[t];
+            }
+            sched_fence();
+        }
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            const int p = 16 * t + l16;
+            if (p < NREG) {
+                const int er = p / EC, ec = p - er * EC;
+                const int gy = ey0 + er, gx = ex0 + ec;
+                const bool inmap = gy >= 0 && gy < H2 && gx >= 0 && gx < W2;
+                f4 v = acc[t];
+                /* max(r16(v), 0) == r16(max(v, 0)): fp16 rounding is monotonic */
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.f);
+                *reinterpret_cast<h4*>(e2s + p * L2 + 16 * wave + 4 * g) = inmap ? cvt_h4(v) : h4{};
+            }
+        }
+    }
+    __syncthreads(); /* the region is complete; the e1 window is dead */
+    /* ---- this block's e2 pixels (region rows and columns 1 .. 2 BR, 2 BC) to the e2 map */
+    {
+        uint16_t* e2 = a2.out + (int64_t)blockIdx.y * a2.out_frame;
+        constexpr int CPP = C2 / 8;
+        for (int q = threadIdx.x; q < 4 * NPX * CPP; q += 64 * NW) {
+            const int pl = q / CPP, c8 = (q - pl * CPP) * 8;
+            const int er = 1 + pl / (2 * BC), ec = 1 + pl % (2 * BC);
+            const int gy = ey0 + er, gx = ex0 + ec;
+            if (gy < H2 && gx < W2)
+                *reinterpret_cast<h8*>(e2 + ((int64_t)gy * W2 + gx) * C2 + c8) =
+                    *reinterpret_cast<const h8*>(e2s + (er * EC + ec) * L2 + c8);
+        }
+    }
+    /* ---- enc3 for the block: pixel group wave / KSP (16 pixels, row-major
+       over the block), k-steps kq, kq + KSP, ... for wave position kq */
+    CodecPix px[TT3];
+    {
+        const int pl = 16 * (wave / KSP) + l16;
+        px[0].y = y3 + pl / BC;
+        px[0].x = x3 + pl % BC;
+        px[0].valid = px[0].y < H3 && px[0].x < W3;
+    }
+    using Src = SrcRegionLds<C2, EC, L2>;
+    const Src src{e2s, y3, x3};
+    f4 acc[RT3][TT3];
+    codec_gemm<Src, RT3, RT3, TT3, KSP>(src, a3.w, a3.b, px, g, lane, 0, acc, wave % KSP);
+    f4* part = reinterpret_cast<f4*>(win);
+    f16* otile = win + NW * NO * TT3 * 64 * 8;
+    codec_ksplit_reduce<RT3, TT3, KSP, LDO>(acc, part, otile, wave, lane, l16, g);
+    __syncthreads();
+    uint16_t* e3 = a3.out + (int64_t)blockIdx.y * a3.out_frame;
+    constexpr int OPP = C3 / 8;
+    for (int q = threadIdx.x; q < NPX * OPP; q += 64 * NW) {
+        const int pl = q / OPP, c8 = (q - pl * OPP) * 8;
+        const int y = y3 + pl / BC, x = x3 + pl % BC;
+        if (y < H3 && x < W3)
+            *reinterpret_cast<h8*>(e3 + ((int64_t)y * W3 + x) * C3 + c8) =
+                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
+    }
+}
+
 #define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))
 #define CODEC_IN_MAP MapSrc(CODEC_FRAME(a.in, a.in_frame), (uint32_t)(a.in_frame * 2))
 #define CODEC_SKIP_MAP MapSrc(CODEC_FRAME(a.skip, a.skip_frame), (uint32_t)(a.skip_frame * 2))
@@ -830,6 +1006,9 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc0(CodecArgs a) { codec_enc0_body(a); }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc01(CodecArgs a0, CodecArgs a1) {
     codec_enc01<CODEC_ENC01_ROWS, CODEC_ENC01_COLS>(a0, a1);
+}
+extern "C" __global__ void __launch_bounds__(512) prism_codec_enc23(CodecArgs a2, CodecArgs a3) {
+    codec_enc23<CODEC_ENC23_ROWS, CODEC_ENC23_COLS, CODEC_ENC23_BAND>(a2, a3);
 }
 extern "C" __global__ void __launch_bounds__(256) prism_codec_enc1(CodecArgs a) {
     codec_stage_any<SrcConvNHWC<32, 2>, 64, CODEC_TT_ENC1, CODEC_RS_ENC1, CODEC_KSP_ENC1, true>(a, SrcConvNHWC<32, 2>{CODEC_IN_MAP, a.in_w, a.in_h});
