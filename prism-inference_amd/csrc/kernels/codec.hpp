@@ -490,6 +490,42 @@ __device__ __forceinline__ void codec_dec21_out(const CodecArgs& a2, const Codec
     codec_out_shuffle<TT>(a1, px, acc, g, lane);
 }
 
+/* The frame window under a block: FR x FC pixels of the 9-channel CHW frame
+ * from pixel (gy0, gx0), into LDS as 16 halfs a pixel (channels 9-15 zero;
+ * zeros where the window leaves the frame), by 256 threads. Every load of a
+ * thread is issued before its first LDS store, so the window costs one memory
+ * round trip; a load for a pixel outside the frame reads pixel 0, and its
+ * value is replaced by zero. */
+template <int FR, int FC>
+__device__ __forceinline__ void codec_frame_window(const f16* frame, int W0, int H0, int gy0, int gx0, f16* s_in) {
+    constexpr int NPX = FR * FC, IT = (NPX + 255) / 256, CH = 9, CP = 16;
+    const int64_t plane = (int64_t)W0 * H0;
+    f16 v[IT][CH];
+    bool ok[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int px = min((int)threadIdx.x + 256 * it, NPX - 1);
+        const int r = px / FC, x = px - r * FC;
+        const int gy = gy0 + r, gx = gx0 + x;
+        ok[it] = gy >= 0 && gy < H0 && gx >= 0 && gx < W0;
+        const f16* src = frame + (ok[it] ? (int64_t)gy * W0 + gx : 0);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[it][c] = src[c * plane];
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int px = threadIdx.x + 256 * it;
+        if (px < NPX) {
+            h8 lo, hi = {};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) lo[c] = ok[it] ? v[it][c] : (f16)0.f;
+            hi[0] = ok[it] ? v[it][8] : (f16)0.f;
+            *reinterpret_cast<h8*>(s_in + px * CP) = lo;
+            *reinterpret_cast<h8*>(s_in + px * CP + 8) = hi;
+        }
+    }
+}
+
 /* enc0: conv3x3 9 -> 32 + ReLU straight from the CHW frame. A workgroup
  * takes a block of CODEC_ENC0_ROWS x 64 output pixels (wave w: row w, 4 tiles
  * of 16 columns). The block's input window with its 1-pixel halo is first
@@ -510,20 +546,8 @@ __device__ __forceinline__ void codec_enc0_body(const CodecArgs& a) {
     const int bxn = (W + CODEC_ENC0_COLS - 1) / CODEC_ENC0_COLS;
     const int blk = codec_block<true>();
     const int by0 = (blk / bxn) * CODEC_ENC0_ROWS, bx0 = (blk % bxn) * CODEC_ENC0_COLS;
-    const f16* frame = reinterpret_cast<const f16*>(a.in) + (int64_t)blockIdx.y * a.in_frame;
-    const int64_t plane = (int64_t)W * H;
-    for (int px = threadIdx.x; px < IR * IC; px += 256) {
-        const int r = px / IC, x = px - r * IC;
-        const int gy = by0 - 1 + r, gx = bx0 - 1 + x;
-        const bool ok = gy >= 0 && gy < H && gx >= 0 && gx < W;
-        const f16* src = frame + (ok ? (int64_t)gy * W + gx : 0);
-        h8 lo, hi = {};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) lo[c] = ok ? src[c * plane] : (f16)0.f;
-        hi[0] = ok ? src[8 * plane] : (f16)0.f;
-        *reinterpret_cast<h8*>(s_in + px * CP) = lo;
-        *reinterpret_cast<h8*>(s_in + px * CP + 8) = hi;
-    }
+    codec_frame_window<IR, IC>(reinterpret_cast<const f16*>(a.in) + (int64_t)blockIdx.y * a.in_frame, W, H, by0 - 1,
+                               bx0 - 1, s_in);
     __syncthreads();
     const FragSrc wsrc(a.w, 2u * KS * 1024u);
     f4 acc[2][TT];
@@ -748,22 +772,8 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
     const int y1 = (blk / bxn) * BR, x1 = (blk % bxn) * BC; /* r1 block origin */
     const int ey0 = 2 * y1 - 1, ex0 = 2 * x1 - 1;          /* e0 region origin */
     /* ---- the frame window (origin ey0 - 1, ex0 - 1), 16 halfs a pixel */
-    {
-        const f16* frame = reinterpret_cast<const f16*>(a0.in) + (int64_t)blockIdx.y * a0.in_frame;
-        const int64_t plane = (int64_t)W0 * H0;
-        for (int px = threadIdx.x; px < FR * FC; px += 256) {
-            const int r = px / FC, x = px - r * FC;
-            const int gy = ey0 - 1 + r, gx = ex0 - 1 + x;
-            const bool ok = gy >= 0 && gy < H0 && gx >= 0 && gx < W0;
-            const f16* src = frame + (ok ? (int64_t)gy * W0 + gx : 0);
-            h8 lo, hi = {};
-#pragma unroll
-            for (int c = 0; c < 8; ++c) lo[c] = ok ? src[c * plane] : (f16)0.f;
-            hi[0] = ok ? src[8 * plane] : (f16)0.f;
-            *reinterpret_cast<h8*>(s_in + px * CP) = lo;
-            *reinterpret_cast<h8*>(s_in + px * CP + 8) = hi;
-        }
-    }
+    codec_frame_window<FR, FC>(reinterpret_cast<const f16*>(a0.in) + (int64_t)blockIdx.y * a0.in_frame, W0, H0,
+                               ey0 - 1, ex0 - 1, s_in);
     __syncthreads();
     /* ---- enc0 for the region; wave w takes region tiles w, w + 4, ... */
     {
