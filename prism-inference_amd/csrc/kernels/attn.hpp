@@ -219,7 +219,11 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             const int q = threadIdx.x + k * NT, sl = q / (UIN / 8), c8 = (q % (UIN / 8)) * 8;
             const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
             const bool ok = gy < a.H && gx < a.W;
-            erow[k] = ok ? *reinterpret_cast<const h8*>(in + (int64_t)(gy * a.W + gx) * UIN + c8) : h8{};
+            /* a padded slot reads slot 0's row (in the map) and takes zeros:
+               no branch around the load, so all of them go out together */
+            const int pix = ok ? gy * a.W + gx : wy * 8 * a.W + wxx * 8;
+            const h8 v = *reinterpret_cast<const h8*>(in + (int64_t)pix * UIN + c8);
+            erow[k] = ok ? v : h8{};
         }
         const FragSrc src_up(a.up_w, (unsigned)(DIM * UIN * 2));
 #pragma unroll
@@ -239,17 +243,42 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
      * block's expert stage of the previous chain, has finished) */
     if (NPT > 0 && a.zero_next && blockIdx.x == 0 && threadIdx.x < a.n_experts)
         a.zero_next[threadIdx.x * a.count_stride] = 0;
-    /* every parameter is staged here, before LN1: loads retire in issue
-     * order, so these LDS stores wait only for the rows and the ring's first
-     * fragments, which LN1 and the QKV GEMM wait for anyway. The barrier
-     * after LN1 publishes them (each wave starts its LN1 as soon as its own
-     * rows are in, without waiting for the other waves' stores) */
-    for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv[i] = a.bqkv[i];
-    if constexpr (PAD)
-        for (int i = threadIdx.x; i < 3 * DIM; i += NT) s_bqkv_pad[i] = a.bqkv_pad[i];
-    for (int i = threadIdx.x; i < DIM; i += NT) s_bo[i] = a.bo[i];
-    if constexpr (NPT > 0)
-        for (int i = threadIdx.x; i < 16 * NPT; i += NT) s_br[i] = a.br[i];
+    /* every parameter is staged here, before LN1. All of a thread's
+     * parameter loads are issued before its first LDS store (a loop of
+     * load-then-store passes waits one L2 round trip per pass); loads retire
+     * in issue order, so the stores wait for the rows, the ring's first
+     * fragments and these loads together: one memory round trip, which LN1
+     * and the QKV GEMM wait for anyway. The barrier after LN1 publishes them
+     * (each wave starts its LN1 as soon as its own rows are in, without
+     * waiting for the other waves' stores) */
+    {
+        constexpr int NQ = (3 * DIM + NT - 1) / NT, NB = (DIM + NT - 1) / NT;
+        constexpr int NR = NPT > 0 ? (16 * NPT + NT - 1) / NT : 0, NRA = NR > 0 ? NR : 1;
+        const int tid = (int)threadIdx.x;
+        float pq[NQ], pp[NQ], pb[NB], pr[NRA];
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) pq[k] = a.bqkv[min(tid + k * NT, 3 * DIM - 1)];
+        if constexpr (PAD) {
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) pp[k] = a.bqkv_pad[min(tid + k * NT, 3 * DIM - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < NB; ++k) pb[k] = a.bo[min(tid + k * NT, DIM - 1)];
+#pragma unroll
+        for (int k = 0; k < NR; ++k) pr[k] = a.br[min(tid + k * NT, 16 * NPT - 1)];
+#pragma unroll
+        for (int k = 0; k < NQ; ++k)
+            if (tid + k * NT < 3 * DIM) {
+                s_bqkv[tid + k * NT] = pq[k];
+                if constexpr (PAD) s_bqkv_pad[tid + k * NT] = pp[k];
+            }
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+            if (tid + k * NT < DIM) s_bo[tid + k * NT] = pb[k];
+#pragma unroll
+        for (int k = 0; k < NR; ++k)
+            if (tid + k * NT < 16 * NPT) s_br[tid + k * NT] = pr[k];
+    }
     if (!up) {
         if (lnw) {
 #pragma unroll

@@ -490,6 +490,33 @@ __device__ __forceinline__ void codec_dec21_out(const CodecArgs& a2, const Codec
     codec_out_shuffle<TT>(a1, px, acc, g, lane);
 }
 
+/* An NHWC map's window (WR x WC pixels of CIN channels from pixel (gy0, gx0))
+ * into LDS, LDE halfs a pixel, zeros where it leaves the map, by NT threads.
+ * Every load of a thread is issued before its first LDS store, so the window
+ * costs one memory round trip (a loop with a guarded load and a store per
+ * pass costs one per pass); loads outside the map read zero through the
+ * buffer resource. */
+template <int CIN, int WR, int WC, int LDE, int NT>
+__device__ __forceinline__ void codec_map_window(const MapSrc& m, int W, int H, int gy0, int gx0, f16* lds) {
+    constexpr int CPP = CIN / 8, N = WR * WC * CPP, IT = (N + NT - 1) / NT;
+    h8 v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int q = (int)threadIdx.x + NT * it;
+        const int px = q / CPP, c8 = (q - px * CPP) * 8;
+        const int r = px / WC, c = px - r * WC;
+        const int gy = gy0 + r, gx = gx0 + c;
+        const bool ok = q < N && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        v[it] = m.load(ok ? (uint32_t)(((gy * W + gx) * CIN + c8) * 2) : CODEC_OOB);
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int q = (int)threadIdx.x + NT * it;
+        const int px = q / CPP, c8 = (q - px * CPP) * 8;
+        if (q < N) *reinterpret_cast<h8*>(lds + px * LDE + c8) = v[it];
+    }
+}
+
 /* The frame window under a block: FR x FC pixels of the 9-channel CHW frame
  * from pixel (gy0, gx0), into LDS as 16 halfs a pixel (channels 9-15 zero;
  * zeros where the window leaves the frame), by 256 threads. Every load of a
@@ -608,7 +635,7 @@ __device__ __forceinline__ void codec_conv_window(const CodecArgs& a) {
     constexpr int WR = 2 * BR + 1, WC = 2 * BC + 1, LDE = CIN + 8; /* window, LDS pixel stride (halfs) */
     constexpr int NPX = BR * BC, TT = NPX / 16, TPR = BC / 16;
     constexpr int RTALL = COUT / 16, RT = RTALL / 4, CPT = CIN / 32, KS = 9 * CPT;
-    constexpr int CPP = CIN / 8, LDO = COUT + 8;
+    constexpr int LDO = COUT + 8;
     static_assert(BC % 16 == 0 && RTALL % 4 == 0 && CIN % 32 == 0 && DW >= 1 && DW <= KS, "window stage shape");
     static_assert(WR * WC * LDE >= NPX * LDO, "the output tile fits where the window was");
     __shared__ __attribute__((aligned(16))) f16 win[WR * WC * LDE];
@@ -620,15 +647,8 @@ __device__ __forceinline__ void codec_conv_window(const CodecArgs& a) {
     const int blk = codec_block<BAND>();
     const int oy0 = (blk / bxn) * BR, ox0 = (blk % bxn) * BC;
     const int wy0 = 2 * oy0 - 1, wx0 = 2 * ox0 - 1;
-    const uint16_t* in = a.in + (int64_t)blockIdx.y * a.in_frame;
-    for (int q = threadIdx.x; q < WR * WC * CPP; q += 256) {
-        const int px = q / CPP, c8 = (q - px * CPP) * 8;
-        const int r = px / WC, c = px - r * WC;
-        const int gy = wy0 + r, gx = wx0 + c;
-        const bool ok = gy >= 0 && gy < ih && gx >= 0 && gx < iw;
-        *reinterpret_cast<h8*>(win + px * LDE + c8) =
-            ok ? *reinterpret_cast<const h8*>(in + ((int64_t)gy * iw + gx) * CIN + c8) : h8{};
-    }
+    codec_map_window<CIN, WR, WC, LDE, 256>(
+        MapSrc(a.in + (int64_t)blockIdx.y * a.in_frame, (uint32_t)(a.in_frame * 2)), iw, ih, wy0, wx0, win);
     __syncthreads();
     const int rt0 = wave * RT;
     f4 acc[RT][TT];
@@ -896,18 +916,8 @@ __device__ __forceinline__ void codec_enc23(const CodecArgs& a2, const CodecArgs
     const int ey0 = 2 * y3 - 1, ex0 = 2 * x3 - 1;          /* e2 region origin */
     const int wy0 = 2 * ey0 - 1, wx0 = 2 * ex0 - 1;        /* e1 window origin */
     /* ---- the e1 window */
-    {
-        const uint16_t* e1 = a2.in + (int64_t)blockIdx.y * a2.in_frame;
-        constexpr int CPP = C1 / 8;
-        for (int q = threadIdx.x; q < WR * WC * CPP; q += 64 * NW) {
-            const int px = q / CPP, c8 = (q - px * CPP) * 8;
-            const int r = px / WC, c = px - r * WC;
-            const int gy = wy0 + r, gx = wx0 + c;
-            const bool ok = gy >= 0 && gy < H1 && gx >= 0 && gx < W1;
-            *reinterpret_cast<h8*>(win + px * L1 + c8) =
-                ok ? *reinterpret_cast<const h8*>(e1 + ((int64_t)gy * W1 + gx) * C1 + c8) : h8{};
-        }
-    }
+    codec_map_window<C1, WR, WC, L1, 64 * NW>(
+        MapSrc(a2.in + (int64_t)blockIdx.y * a2.in_frame, (uint32_t)(a2.in_frame * 2)), W1, H1, wy0, wx0, win);
     __syncthreads();
     /* ---- enc2 for the region: wave w takes row tile w over all NT2 tiles */
     {

@@ -95,22 +95,24 @@ __device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int lane, i
 }
 
 /* Stages expert e's biases and the tile's token ids (-1 past the segment's
- * end, and for a bucket entry that names no token). The caller synchronises. */
+ * end, and for a bucket entry that names no token); rows >= 1. A thread's
+ * three loads (b1, b2, its bucket entry; clamped indices, the values past
+ * the ends unused) are all issued before its first LDS store, so staging
+ * costs one memory round trip. The caller synchronises. */
 template <int DIM, int BM, int NT>
 __device__ __forceinline__ void expert_stage_tile(const ExpertArgs& a, int e, int row0, int rows, float* s_b1,
                                                   float* s_b2, int* tok) {
-    for (int i = threadIdx.x; i < DIM; i += NT) {
-        s_b1[i] = a.b1[(int64_t)e * DIM + i];
-        s_b2[i] = a.b2[(int64_t)e * DIM + i];
+    static_assert(DIM <= NT && BM <= NT, "one bias entry and one row a thread");
+    const int i = (int)threadIdx.x, ic = min(i, DIM - 1);
+    const float b1 = a.b1[(int64_t)e * DIM + ic], b2 = a.b2[(int64_t)e * DIM + ic];
+    int t = row0 + i;
+    if (a.counts) t = a.perm[(int64_t)e * a.cap + row0 + min(i, rows - 1)]; /* uniform branch */
+    if (i >= rows || t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
+    if (i < DIM) {
+        s_b1[i] = b1;
+        s_b2[i] = b2;
     }
-    for (int r = threadIdx.x; r < BM; r += NT) {
-        int t = -1;
-        if (r < rows) {
-            t = a.counts ? a.perm[(int64_t)e * a.cap + row0 + r] : row0 + r;
-            if (t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
-        }
-        tok[r] = t;
-    }
+    if (i < BM) tok[i] = t;
 }
 
 template <int DIM, int BM, int NW>
@@ -247,12 +249,18 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         static_assert(DRT >= 1, "down-projection shape");
         const bool dn = a.dn_w != nullptr; /* uniform over the launch */
         h8 wd[DRT][KS];
+        f4 dbias[DRT];
         if (dn) {
             const FragSrc src_dn(a.dn_w, (unsigned)(DO * DIM * 2));
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
                 for (int r = 0; r < DRT; ++r) wd[r][ks] = src_dn.load((wave * DRT + r) * KS + ks, loff);
+#pragma unroll
+            for (int r = 0; r < DRT; ++r) {
+                const int ch = (wave * DRT + r) * 16 + 4 * g;
+                dbias[r] = f4{a.dn_b[ch], a.dn_b[ch + 1], a.dn_b[ch + 2], a.dn_b[ch + 3]};
+            }
         }
         /* epilogue: y = r16(W2 g + b2), out = y + h in fp16 (one rounding),
          * written over the lane's own residual in hs, then whole rows out */
@@ -272,12 +280,9 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
              * tile in hs into xs (free since GEMM2), then 128-channel rows out */
             f4 dacc[DRT][TT];
 #pragma unroll
-            for (int r = 0; r < DRT; ++r) {
-                const int ch = (wave * DRT + r) * 16 + 4 * g;
-                const f4 bb = {a.dn_b[ch], a.dn_b[ch + 1], a.dn_b[ch + 2], a.dn_b[ch + 3]};
+            for (int r = 0; r < DRT; ++r)
 #pragma unroll
-                for (int t = 0; t < TT; ++t) dacc[r][t] = bb;
-            }
+                for (int t = 0; t < TT; ++t) dacc[r][t] = dbias[r];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll

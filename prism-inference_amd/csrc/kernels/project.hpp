@@ -36,14 +36,17 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
     const int64_t ntiles = (a.n_tokens + 63) / 64;
 
     /* the rows of token tile `tile` (one contiguous block): 16 bytes per
-     * lane, whole cache lines per wave load; rows past the end read as zero */
+     * lane, whole cache lines per wave load; rows past the end read the
+     * tile's last row (no branch around the loads, so they go out together)
+     * and are kept as zero */
     auto load_rows = [&](int64_t tile, h8 (&x)[EI]) {
         const int64_t tok0 = tile * 64;
         const int rows = (int)min<int64_t>(64, a.n_tokens - tok0);
 #pragma unroll
         for (int k = 0; k < EI; ++k) {
             const int q = threadIdx.x + 256 * k, r = q / (IN / 8), c8 = (q % (IN / 8)) * 8;
-            x[k] = r < rows ? *reinterpret_cast<const h8*>(a.in + (tok0 + r) * IN + c8) : h8{};
+            const h8 v = *reinterpret_cast<const h8*>(a.in + (tok0 + min(r, rows - 1)) * IN + c8);
+            x[k] = r < rows ? v : h8{};
         }
     };
     int64_t tile = blockIdx.x;

@@ -30,10 +30,15 @@
 
 template <int DIM, int KS>
 __device__ __forceinline__ void router_load_tile(const RouterArgs& a, int token, int g, h8 (&xr)[KS]) {
-    const uint16_t* row = a.in + (int64_t)(token < a.n_tokens ? token : 0) * DIM;
+    /* past the last token: token 0's row is read (no branch around the
+       loads, so they go out together) and zeros are kept */
+    const bool ok = token < a.n_tokens;
+    const uint16_t* row = a.in + (int64_t)(ok ? token : 0) * DIM;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-        xr[ks] = token < a.n_tokens ? *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g) : h8{};
+    for (int ks = 0; ks < KS; ++ks) {
+        const h8 v = *reinterpret_cast<const h8*>(row + 32 * ks + 8 * g);
+        xr[ks] = ok ? v : h8{};
+    }
 }
 
 template <int DIM, int NPT>
@@ -59,11 +64,21 @@ __device__ __forceinline__ void router_body(const RouterArgs& a) {
     h8 xr[KS];
     router_load_tile<DIM, KS>(a, tok_wg0 + wave * tpw * 16 + l16, g, xr);
     {
+        /* every load of the copy is issued before its first LDS store (one
+           memory round trip, not one per pass) */
+        static_assert(NF * 64 % 256 == 0 && 16 * NPT <= 256, "whole passes");
+        constexpr int NP = NF * 64 / 256;
         const FragSrc src_r(a.wr, 16u * NPT * DIM * 2u);
-        for (int i = threadIdx.x; i < NF * 64; i += 256) s_wr[i] = src_r.load(i / 64, (i % 64) * 16);
+        const int tid = (int)threadIdx.x;
+        h8 v[NP];
+#pragma unroll
+        for (int k = 0; k < NP; ++k) v[k] = src_r.load((tid + 256 * k) / 64, ((tid + 256 * k) % 64) * 16);
+        const float br = a.br[min(tid, 16 * NPT - 1)];
+#pragma unroll
+        for (int k = 0; k < NP; ++k) s_wr[tid + 256 * k] = v[k];
+        if (tid < 16 * NPT) s_br[tid] = br;
     }
     if (threadIdx.x < 64) hist[threadIdx.x] = 0;
-    for (int i = threadIdx.x; i < 16 * NPT; i += 256) s_br[i] = a.br[i];
     __syncthreads();
 
 #pragma unroll 1
