@@ -173,9 +173,12 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     const FragSrc src_r(NPT > 0 ? a.wr : a.wo, NPT > 0 ? 16u * NPT * DIM * 2u : 0u);
     const int loff = lane * 16;
     /* waves 0-3 route tiles 0-3 of the window (waves w and w+4 tile w % 4
-     * when split); only they stream W_r */
+     * when split). Every wave's ring runs into W_r's first fragments (the
+     * refills are unconditional: a refill under a wave-dependent branch makes
+     * the compiler's load counting at the join wait for the refills just
+     * issued, a full L2 round trip per k-step at the end of the
+     * out-projection); only the routing waves consume them. */
     const bool routes = NPT > 0 && (S::RSPLIT ? (wave & 3) < TQ : wave < TQ);
-    const int total = routes ? S::TOTAL : S::RBASE;
 
     /* ---- 1. LN1 --------------------------------------------------------
      * The window's rows (HBM) are requested first, then the weight ring and
@@ -266,18 +269,18 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         for (int k = 0; k < NB; ++k) pb[k] = a.bo[min(tid + k * NT, DIM - 1)];
 #pragma unroll
         for (int k = 0; k < NR; ++k) pr[k] = a.br[min(tid + k * NT, 16 * NPT - 1)];
+        /* the stores are unconditional: a thread past an array's end writes
+           its last entry with the value it holds (the same value), so no
+           branch invites the compiler to sink a load next to its store */
 #pragma unroll
-        for (int k = 0; k < NQ; ++k)
-            if (tid + k * NT < 3 * DIM) {
-                s_bqkv[tid + k * NT] = pq[k];
-                if constexpr (PAD) s_bqkv_pad[tid + k * NT] = pp[k];
-            }
+        for (int k = 0; k < NQ; ++k) {
+            s_bqkv[min(tid + k * NT, 3 * DIM - 1)] = pq[k];
+            if constexpr (PAD) s_bqkv_pad[min(tid + k * NT, 3 * DIM - 1)] = pp[k];
+        }
 #pragma unroll
-        for (int k = 0; k < NB; ++k)
-            if (tid + k * NT < DIM) s_bo[tid + k * NT] = pb[k];
+        for (int k = 0; k < NB; ++k) s_bo[min(tid + k * NT, DIM - 1)] = pb[k];
 #pragma unroll
-        for (int k = 0; k < NR; ++k)
-            if (tid + k * NT < 16 * NPT) s_br[tid + k * NT] = pr[k];
+        for (int k = 0; k < NR; ++k) s_br[min(tid + k * NT, 16 * NPT - 1)] = pr[k];
     }
     if (!up) {
         if (lnw) {
@@ -388,7 +391,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
                     else if (mat == 1) accK[c][t] = mfma_16x16x32(w, xf[t], accK[c][t]);
                     else accV[t][c] = mfma_16x16x32(xf[t], w, accV[t][c]);
                 }
-                if (p + PF < S::TOTAL && p + PF < total)
+                if (p + PF < S::TOTAL)
                     ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
             }
             if (ks + 1 < KS) {
@@ -547,7 +550,7 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             const h8 w = ring[p % PF];
 #pragma unroll
             for (int t = 0; t < TQ; ++t) acc[r][t] = mfma_16x16x32(w, of[t], acc[r][t]);
-            if (p + PF < S::TOTAL && p + PF < total)
+            if (p + PF < S::TOTAL)
                 ring[p % PF] = attn_frag<DIM, HD, NW, NPT>(src_qkv, src_o, src_r, wave, p + PF, loff);
         }
         if (ks + 1 < KS) {
