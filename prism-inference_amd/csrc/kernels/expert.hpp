@@ -386,7 +386,7 @@ struct ExpertWideLds {
 template <int DIM, int PF, int BM, int TA>
 __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a, ExpertWideLds<DIM, BM>& L, int e, int row0,
                                                  int rows) {
-    constexpr int NW = 4, NT = 64 * NW;
+    constexpr int NW = 4;
     constexpr int KS = DIM / 32;
     constexpr int LDS = DIM + 8;
     constexpr int RT = DIM / 16 / NW; /* 16-row output tiles per wave  */
@@ -416,8 +416,7 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a, ExpertWide
         const int q = p % (RT * KS), ks = q / RT, r = q % RT;
         return (p < RT * KS ? w1 : w2).load((wave * RT + r) * KS + ks, loff);
     };
-    expert_stage_tile<DIM, BM, NT>(a, e, row0, rows, s_b1, s_b2, tok);
-    __syncthreads();
+    /* the tile's biases and token ids are staged by the caller */
 
     /* rows first, then the ring's first fragments; LN2 runs while they arrive */
     RowChunk rc[IT];
@@ -523,6 +522,11 @@ __device__ __forceinline__ void expert_wide(const ExpertArgs& a, ExpertWideLds<D
     int e, row0, rows;
     expert_schedule<BM>(a, lane_id(), e, row0, rows);
     if (e < 0) return;
+    /* staged once ahead of the body choice (staged inside each body, the
+     * compiler merged the two paths' loads and waited for the biases before
+     * requesting the bucket entries: two round trips instead of one) */
+    expert_stage_tile<DIM, BM, 256>(a, e, row0, rows, L.b1, L.b2, L.tok);
+    __syncthreads();
     if (SHORT && rows <= 64) /* uniform */
         expert_body_wide<DIM, PF, BM, 4>(a, L, e, row0, rows);
     else
