@@ -134,8 +134,10 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     constexpr int NT = 64 * NW;         /* threads                         */
     constexpr int KS = S::KS, CT = S::CT, LDS = S::LDS, ORT = S::ORT;
     /* ring depth: 2 k-steps ahead; 1 in the rare PAD body, whose padded-slot
-     * fix-up needs the registers */
-    constexpr int PF = PAD ? S::FPK : S::PF;
+     * fix-up needs the registers; 4 in the HALF body, whose k-steps have half
+     * the MFMAs to cover an L2 round trip with (and which has half the
+     * accumulators) */
+    constexpr int PF = PAD ? (HALF ? 2 * S::FPK : S::FPK) : (HALF ? 4 * S::FPK : S::PF);
     constexpr float LOG2E = 1.4426950408889634f;
     const float scale = (HD == 32) ? 0.1767766953f : 1.0f / sqrtf((float)HD);
     const float sl2 = scale * LOG2E;
