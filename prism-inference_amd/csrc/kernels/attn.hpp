@@ -583,15 +583,21 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
     auto store_rows = [&]() {
         constexpr int CPR = DIM / 8;  /* 16-byte chunks per row */
         constexpr int RPS = 64 / CPR; /* rows per wave store    */
+        constexpr int NI = SPW / RPS;
         static_assert(64 % CPR == 0 && SPW % RPS == 0, "row store shape");
+        const int c8 = (lane % CPR) * 8;
+        /* every LDS read first, then the stores (a read under the store's
+           condition costs one LDS round trip per row pass) */
+        h8 v[NI];
 #pragma unroll
-        for (int it = 0; it < SPW / RPS; ++it) {
+        for (int it = 0; it < NI; ++it)
+            v[it] = *reinterpret_cast<const h8*>(os + (wave * SPW + it * RPS + lane / CPR) * LDS + c8);
+#pragma unroll
+        for (int it = 0; it < NI; ++it) {
             const int sl = wave * SPW + it * RPS + lane / CPR;
-            const int c8 = (lane % CPR) * 8;
             const int gy = wy * 8 + (sl >> 3), gx = wxx * 8 + (sl & 7);
             if (gy < a.H && gx < a.W)
-                st_row16<NW == 8>(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u,
-                                  *reinterpret_cast<const h8*>(os + sl * LDS + c8));
+                st_row16<NW == 8>(out, ((uint32_t)(gy * a.W + gx) * DIM + c8) * 2u, v[it]);
         }
     };
 

@@ -190,6 +190,30 @@ __device__ __forceinline__ int codec_block() {
     return x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
 }
 
+/* A workgroup's output block from LDS to memory in 16-byte chunks (NPX
+ * pixels of CPP chunks, NT threads). Every LDS read is issued before the
+ * first store: a read under a store's condition costs one LDS round trip per
+ * pass. src(pl): the LDS address of block pixel pl's first channel; dst(pl):
+ * the memory address of its first channel, or nullptr past the map. */
+template <int NPX, int CPP, int NT, class Src, class Dst>
+__device__ __forceinline__ void codec_store_block(Src&& src, Dst&& dst) {
+    constexpr int N = NPX * CPP, IT = (N + NT - 1) / NT;
+    h8 v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int q = min((int)threadIdx.x + NT * it, N - 1);
+        v[it] = *reinterpret_cast<const h8*>(src(q / CPP) + (q % CPP) * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int q = (int)threadIdx.x + NT * it;
+        if (q < N) {
+            uint16_t* d = dst(q / CPP);
+            if (d) *reinterpret_cast<h8*>(d + (q % CPP) * 8) = v[it];
+        }
+    }
+}
+
 /* A workgroup's 4 waves form 4/RS pixel groups of TT tiles each; the RS waves
  * of a group split the output channels. */
 template <int TT, int RS, bool BAND>
@@ -238,12 +262,8 @@ __device__ __forceinline__ void codec_stage(const CodecArgs& a, const Src& src) 
     __syncthreads();
     const int64_t p0 = (int64_t)codec_block<BAND>() * NPX, npix = (int64_t)a.out_w * a.out_h;
     uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
-    constexpr int CPP = COUT / 8; /* 16-byte chunks per pixel */
-    for (int q = threadIdx.x; q < NPX * CPP; q += 256) {
-        const int pl = q / CPP, c8 = (q % CPP) * 8;
-        if (p0 + pl < npix)
-            *reinterpret_cast<h8*>(out + (p0 + pl) * COUT + c8) = *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
-    }
+    codec_store_block<NPX, COUT / 8, 256>([&](int pl) { return otile + pl * LDO; },
+                                          [&](int pl) { return p0 + pl < npix ? out + (p0 + pl) * COUT : nullptr; });
 }
 
 /* One stage with its reduction split over KSP waves (K-split): the
@@ -331,12 +351,8 @@ __device__ __forceinline__ void codec_stage_ksplit(const CodecArgs& a, const Src
     __syncthreads();
     const int64_t p0 = (int64_t)codec_block<BAND>() * NPX, npix = (int64_t)a.out_w * a.out_h;
     uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
-    constexpr int CPP = COUT / 8;
-    for (int q = threadIdx.x; q < NPX * CPP; q += 256) {
-        const int pl = q / CPP, c8 = (q % CPP) * 8;
-        if (p0 + pl < npix)
-            *reinterpret_cast<h8*>(out + (p0 + pl) * COUT + c8) = *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
-    }
+    codec_store_block<NPX, COUT / 8, 256>([&](int pl) { return otile + pl * LDO; },
+                                          [&](int pl) { return p0 + pl < npix ? out + (p0 + pl) * COUT : nullptr; });
 }
 
 /* A stage's kernel body: K-split when KSP > 1, else channels split over RS
@@ -714,14 +730,10 @@ __device__ __forceinline__ void codec_conv_window(const CodecArgs& a) {
         }
     __syncthreads();
     uint16_t* out = a.out + (int64_t)blockIdx.y * a.out_frame;
-    constexpr int OPP = COUT / 8; /* 16-byte chunks a pixel */
-    for (int q = threadIdx.x; q < NPX * OPP; q += 256) {
-        const int pl = q / OPP, c8 = (q - pl * OPP) * 8;
+    codec_store_block<NPX, COUT / 8, 256>([&](int pl) { return otile + pl * LDO; }, [&](int pl) {
         const int y = oy0 + pl / BC, x = ox0 + pl % BC;
-        if (y < oh && x < ow)
-            *reinterpret_cast<h8*>(out + ((int64_t)y * ow + x) * COUT + c8) =
-                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
-    }
+        return y < oh && x < ow ? out + ((int64_t)y * ow + x) * COUT : nullptr;
+    });
 }
 
 /* A stride-2 conv3x3's taps read from an LDS copy of the input region under
@@ -866,13 +878,10 @@ __device__ __forceinline__ void codec_enc01(const CodecArgs& a0, const CodecArgs
         }
     __syncthreads();
     uint16_t* e1map = a1.out + (int64_t)blockIdx.y * a1.out_frame;
-    for (int q = threadIdx.x; q < NPX * 8; q += 256) { /* 16-byte chunks: 8 a pixel */
-        const int pl = q >> 3, c8 = (q & 7) * 8;
+    codec_store_block<NPX, 8, 256>([&](int pl) { return otile + pl * LDO; }, [&](int pl) {
         const int Y = y1 + pl / BC, X = x1 + pl % BC;
-        if (Y < H1 && X < W1)
-            *reinterpret_cast<h8*>(e1map + ((int64_t)Y * W1 + X) * 64 + c8) =
-                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
-    }
+        return Y < H1 && X < W1 ? e1map + ((int64_t)Y * W1 + X) * 64 : nullptr;
+    });
 }
 
 /* enc2 + enc3 in one launch (prism_encode and the end-to-end frame; the stage
@@ -981,15 +990,11 @@ __device__ __forceinline__ void codec_enc23(const CodecArgs& a2, const CodecArgs
     /* ---- this block's e2 pixels (region rows and columns 1 .. 2 BR, 2 BC) to the e2 map */
     {
         uint16_t* e2 = a2.out + (int64_t)blockIdx.y * a2.out_frame;
-        constexpr int CPP = C2 / 8;
-        for (int q = threadIdx.x; q < 4 * NPX * CPP; q += 64 * NW) {
-            const int pl = q / CPP, c8 = (q - pl * CPP) * 8;
-            const int er = 1 + pl / (2 * BC), ec = 1 + pl % (2 * BC);
-            const int gy = ey0 + er, gx = ex0 + ec;
-            if (gy < H2 && gx < W2)
-                *reinterpret_cast<h8*>(e2 + ((int64_t)gy * W2 + gx) * C2 + c8) =
-                    *reinterpret_cast<const h8*>(e2s + (er * EC + ec) * L2 + c8);
-        }
+        codec_store_block<4 * NPX, C2 / 8, 64 * NW>(
+            [&](int pl) { return e2s + ((1 + pl / (2 * BC)) * EC + 1 + pl % (2 * BC)) * L2; }, [&](int pl) {
+                const int gy = ey0 + 1 + pl / (2 * BC), gx = ex0 + 1 + pl % (2 * BC);
+                return gy < H2 && gx < W2 ? e2 + ((int64_t)gy * W2 + gx) * C2 : nullptr;
+            });
     }
     /* ---- enc3 for the block: pixel group wave / KSP (16 pixels, row-major
        over the block), k-steps kq, kq + KSP, ... for wave position kq */
@@ -1009,14 +1014,10 @@ __device__ __forceinline__ void codec_enc23(const CodecArgs& a2, const CodecArgs
     codec_ksplit_reduce<RT3, TT3, KSP, LDO>(acc, part, otile, wave, lane, l16, g);
     __syncthreads();
     uint16_t* e3 = a3.out + (int64_t)blockIdx.y * a3.out_frame;
-    constexpr int OPP = C3 / 8;
-    for (int q = threadIdx.x; q < NPX * OPP; q += 64 * NW) {
-        const int pl = q / OPP, c8 = (q - pl * OPP) * 8;
+    codec_store_block<NPX, C3 / 8, 64 * NW>([&](int pl) { return otile + pl * LDO; }, [&](int pl) {
         const int y = y3 + pl / BC, x = x3 + pl % BC;
-        if (y < H3 && x < W3)
-            *reinterpret_cast<h8*>(e3 + ((int64_t)y * W3 + x) * C3 + c8) =
-                *reinterpret_cast<const h8*>(otile + pl * LDO + c8);
-    }
+        return y < H3 && x < W3 ? e3 + ((int64_t)y * W3 + x) * C3 : nullptr;
+    });
 }
 
 #define CODEC_FRAME(p, n) ((p) + (int64_t)blockIdx.y * (n))

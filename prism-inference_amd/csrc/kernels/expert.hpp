@@ -45,20 +45,27 @@
 /* Writes the output tile (BM rows of C channels in LDS, row stride STRIDE
  * halfs) to the rows of its tokens: each wave stores BM/NW rows, 16 bytes
  * per lane, so one instruction covers 1 KiB of whole rows instead of 16
- * tokens x 32 bytes. */
+ * tokens x 32 bytes. Every LDS read (token ids, then the chunks) is issued
+ * before the first store: a read under the store's condition costs one LDS
+ * round trip per row pass. */
 template <int C, int STRIDE, int BM, int NW, bool NT = false>
 __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile, const int* tok, int wave, int lane) {
     constexpr int CPR = C / 8;    /* 16-byte chunks per row */
     constexpr int RPS = 64 / CPR; /* rows per wave store    */
+    constexpr int NI = BM / NW / RPS;
     static_assert(64 % CPR == 0 && (BM / NW) % RPS == 0, "store shape");
+    const int c8 = (lane % CPR) * 8;
+    int tk[NI];
+    h8 v[NI];
 #pragma unroll
-    for (int it = 0; it < BM / NW / RPS; ++it) {
+    for (int it = 0; it < NI; ++it) {
         const int r = wave * (BM / NW) + it * RPS + lane / CPR;
-        const int c8 = (lane % CPR) * 8;
-        const int tk = tok[r];
-        if (tk >= 0)
-            st_row16<NT>(out, ((uint32_t)tk * C + c8) * 2u, *reinterpret_cast<const h8*>(tile + r * STRIDE + c8));
+        tk[it] = tok[r];
+        v[it] = *reinterpret_cast<const h8*>(tile + r * STRIDE + c8);
     }
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+        if (tk[it] >= 0) st_row16<NT>(out, ((uint32_t)tk[it] * C + c8) * 2u, v[it]);
 }
 
 /* Tile scheduler (see the file comment): every wave finds this workgroup's
@@ -503,14 +510,20 @@ __device__ __forceinline__ void expert_body_wide(const ExpertArgs& a, ExpertWide
     __syncthreads(); /* y tile complete */
     /* ---- out = y + h in fp16 (one rounding), whole rows --------------- */
     if (rw) {
+        /* every LDS read first (token ids and y chunks), then the stores: a
+           read under the store's condition costs one LDS round trip per row
+           pass */
+        int tk[NI];
+        h8 y[NI];
 #pragma unroll
         for (int it = 0; it < NI; ++it) {
             const int r = wave * (BM / NW) + it * RPS + lane / CPR;
-            const int tk = tok[r];
-            if (tk >= 0)
-                st_row16(a.out, ((uint32_t)tk * DIM + c8) * 2u,
-                         add_f16x8(*reinterpret_cast<const h8*>(xs + r * LDS + c8), hx[it]));
+            tk[it] = tok[r];
+            y[it] = *reinterpret_cast<const h8*>(xs + r * LDS + c8);
         }
+#pragma unroll
+        for (int it = 0; it < NI; ++it)
+            if (tk[it] >= 0) st_row16(a.out, ((uint32_t)tk[it] * DIM + c8) * 2u, add_f16x8(y[it], hx[it]));
     }
 }
 

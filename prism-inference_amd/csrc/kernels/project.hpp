@@ -104,11 +104,18 @@ __device__ __forceinline__ void project_body(const ProjArgs& a) {
                 *reinterpret_cast<h4*>(tout + (16 * t + l16) * LO + (wave * RT + r) * 16 + 4 * g) = cvt_h4(v);
             }
         __syncthreads(); /* the output tile is complete; every wave is done reading tin */
+        /* every LDS read first, then the stores (a read under a store's
+           condition costs one LDS round trip per pass) */
+        h8 yo[EO];
 #pragma unroll
         for (int k = 0; k < EO; ++k) {
             const int q = threadIdx.x + 256 * k, r = q / (OUT / 8), c8 = (q % (OUT / 8)) * 8;
-            if (r < rows)
-                *reinterpret_cast<h8*>(a.out + (tok0 + r) * OUT + c8) = *reinterpret_cast<const h8*>(tout + r * LO + c8);
+            yo[k] = *reinterpret_cast<const h8*>(tout + r * LO + c8);
+        }
+#pragma unroll
+        for (int k = 0; k < EO; ++k) {
+            const int q = threadIdx.x + 256 * k, r = q / (OUT / 8), c8 = (q % (OUT / 8)) * 8;
+            if (r < rows) *reinterpret_cast<h8*>(a.out + (tok0 + r) * OUT + c8) = yo[k];
         }
     }
 }
