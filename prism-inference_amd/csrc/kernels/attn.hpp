@@ -561,18 +561,22 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         }
         sched_fence();
     }
+    /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding), over the
+     * residual: the tile leaves the CU as whole rows (below). All of this
+     * lane's residual reads go out before the first add (read-add-write per
+     * element waits one LDS round trip each) */
+    h4 xres[4][ORT];
 #pragma unroll
-    for (int t = 0; t < TQ; ++t) {
-        const int sl = 16 * t + l16;
+    for (int t = 0; t < TQ; ++t)
 #pragma unroll
-        for (int r = 0; r < ORT; ++r) {
-            const int ch = (wave * ORT + r) * 16 + 4 * g;
-            h4* xr = reinterpret_cast<h4*>(os + sl * LDS + ch); /* this lane's residual, read once */
-            /* po = r16(Wo a + bo); y = po + x in fp16 (one rounding), over
-             * the residual: the tile leaves the CU as whole rows (below) */
-            *xr = add_f16x4(cvt_h4(acc[r][t]), *xr);
-        }
-    }
+        for (int r = 0; r < ORT; ++r)
+            xres[t][r] = *reinterpret_cast<const h4*>(os + (16 * t + l16) * LDS + (wave * ORT + r) * 16 + 4 * g);
+#pragma unroll
+    for (int t = 0; t < TQ; ++t)
+#pragma unroll
+        for (int r = 0; r < ORT; ++r)
+            *reinterpret_cast<h4*>(os + (16 * t + l16) * LDS + (wave * ORT + r) * 16 + 4 * g) =
+                add_f16x4(cvt_h4(acc[r][t]), xres[t][r]);
     __syncthreads(); /* y tile complete in os */
     /* ---- 6. y rows out, 16 bytes per lane (a wave store covers whole rows).
      * Loads and stores retire through one counter (vmcnt), so a load or a

@@ -272,13 +272,20 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
         }
         /* epilogue: y = r16(W2 g + b2), out = y + h in fp16 (one rounding),
          * written over the lane's own residual in hs, then whole rows out */
+        /* every residual read first, then the adds (read-add-write per
+         * element waits one LDS round trip each) */
+        h4 hres[TT][RT];
 #pragma unroll
         for (int t = 0; t < TT; ++t)
 #pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                h4* hp = reinterpret_cast<h4*>(hs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g);
-                *hp = add_f16x4(cvt_h4(acc[r][t]), *hp);
-            }
+            for (int r = 0; r < RT; ++r)
+                hres[t][r] = *reinterpret_cast<const h4*>(hs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g);
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                *reinterpret_cast<h4*>(hs + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g) =
+                    add_f16x4(cvt_h4(acc[r][t]), hres[t][r]);
         __syncthreads();
         if (!dn) {
             expert_store_rows<DIM, LDS, BM, NW, NW == 8>(a.out, hs, tok, wave, lane);
