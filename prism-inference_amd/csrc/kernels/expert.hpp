@@ -115,9 +115,9 @@ __device__ __forceinline__ void expert_stage_tile(const ExpertArgs& a, int e, in
     int t = row0 + i;
     if (a.counts) t = a.perm[(int64_t)e * a.cap + row0 + min(i, rows - 1)]; /* uniform branch */
     if (i >= rows || t < 0 || t >= a.n_tokens) t = -1; /* never follow a stale bucket entry */
-    /* unconditional stores (a thread past an end writes the last entry with
-       the value it holds, the same one), so no branch invites the compiler
-       to sink a load next to its store */
+    /* the bias stores are unconditional (a thread past the end writes the
+       last entry with the value it holds, the same one), so no branch
+       invites the compiler to sink their loads next to them */
     s_b1[ic] = b1;
     s_b2[ic] = b2;
     if (i < BM) tok[i] = t;
