@@ -3,8 +3,8 @@ the C ABI, against the oracle.
 
 - Free-running: prism_forward_graph over the whole model (MoE-32: 22 blocks at
   135x240, batch 4, adversarial routing; MoE-16: 16 blocks at 68x120; MoE-64:
-  16 blocks at 68x120, batch 16 = the headline step) against the free-running
-  oracle. Near-tie routing flips move a few tokens by more than the per-block
+  16 blocks at 68x120, batch 16 = the headline step; dense128 and std256 at
+  batch 16) against the free-running oracle. Near-tie routing flips move a few tokens by more than the per-block
   bound, so the whole-model check bounds the mean error (2e-3) and the share
   of tokens moved by more than 2e-2 (2 %).
 - Teacher-forced through the chain's own kernels: the chain runs a batch of 4
@@ -58,6 +58,7 @@ def attn_kernel(dim, n_experts, windows):
     ("moe16", 1, "prism_attn_d256_w8_r1"),
     ("moe64", 16, "prism_attn_d256_r4"),  # the headline step: 2 x 8 frames, 1080 windows each
     ("dense128", 16, "prism_attn_d128"),  # 2 x 8 frames of 1080 windows, dense FFN
+    ("std256", 16, "prism_attn_d256"),    # 2 x 8 frames: the dense FFN in 128-token tiles
 ])
 def test_config_chain_against_oracle(hip, engine, device_arena, name, batch, kernel):
     cfg = P.CONFIGS[name]
