@@ -54,6 +54,13 @@ static_assert(CHAIN_SPLIT >= 1 && CHAIN_SPLIT <= 4, "sub-chain streams");
  * sub-chain's attention launch fills that round, and 128-token tiles stay
  * ahead there. */
 static constexpr int EXPERT_WIDE_MIN_TILES = 512;
+/* The share of the 256 MB memory-side cache the weights may keep across
+ * small-batch frames: when a model's weights exceed it, the 8-wave 64-token
+ * expert kernel (the small grids of batch 1-2) reads the expert weights of
+ * the first blocks non-temporally, so the rest stays resident from one frame
+ * to the next instead of the whole cyclic stream missing (prism_load_weights
+ * sets wnt_blocks). */
+static constexpr int64_t WEIGHT_CACHE_KEEP = 224ll << 20;
 /* Workgroups of a projection stage launch (persistent, 64-token tiles in a
  * loop; the d256 kernels' 210-220 VGPRs allow two per CU). At batch 16,
  * 68x120, up 128->256: 512 workgroups 18.5 us, 384 20.6, 256 23.5, 1024
@@ -101,6 +108,7 @@ struct prism_ctx {
     prism_model_desc desc{};
     void* warena = nullptr;
     std::vector<DevBlock> blocks;
+    int wnt_blocks = 0; /* leading blocks whose expert weights stream non-temporally */
 
     /* projection adapters (prism_load_adapters) */
     void* aarena = nullptr;

@@ -352,6 +352,14 @@ extern "C" int prism_load_weights(prism_ctx* c, const prism_model_desc* d, const
     if (c->desc.dim != d->dim) drop_adapters(c);
     if (c->desc.spatial_h != d->spatial_h || c->desc.spatial_w != d->spatial_w) codec_release(c);
     c->desc = *d;
+    {
+        /* leading blocks whose expert weights the 64-token kernels stream
+           past the memory-side cache: enough of them that the rest of the
+           arena fits the share it may keep */
+        const int64_t excess = (int64_t)ar.off - WEIGHT_CACHE_KEEP;
+        const int64_t per_block = (int64_t)d->n_experts * 2 * D * D * 2;
+        c->wnt_blocks = excess > 0 ? (int)std::min<int64_t>(d->n_blocks, (excess + per_block - 1) / per_block) : 0;
+    }
     c->loaded = true;
     return PRISM_OK;
 }
@@ -548,7 +556,7 @@ int enqueue_router(prism_ctx* c, const DevBlock& k, const uint16_t* in, int32_t*
 
 int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, const int32_t* counts,
                     const int32_t* perm, int64_t n, hipStream_t s, int32_t count_stride = 1, bool dn = false,
-                    bool stage = false) {
+                    bool stage = false, bool wnt = false) {
     const int D = c->desc.dim, N = counts ? c->desc.n_experts : 1;
     ExpertArgs a{};
     if (dn) { /* the adapted chain's last block: 128-channel output rows */
@@ -567,6 +575,7 @@ int enqueue_experts(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_
     a.n_experts = N;
     a.cap = (int32_t)n;
     a.count_stride = count_stride;
+    a.wnt = wnt ? 1 : 0;
     /* tiles: the worst case of ceil(n / bm) + one partial tile per expert,
      * a multiple of 8 (the kernels' XCD-major tile order) */
     auto tiles_of = [&](int64_t bm) { return ((n + bm - 1) / bm + (counts ? N : 0) + 7) / 8 * 8; };
@@ -916,7 +925,9 @@ static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int 
                               NB > 1 ? counts0 + (size_t)((b + 1) % NB) * row : nullptr};
             int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, &ro, first);
             if (!rc) rc = timer_mark(c, tm, 0, s);
-            if (!rc) rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last);
+            if (!rc)
+                rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last, false,
+                                     b < c->wnt_blocks);
             if (!rc) rc = timer_mark(c, tm, 1, s);
             if (rc) return rc;
         } else {

@@ -93,6 +93,9 @@ typedef struct ExpertArgs {
      * 128-channel rows */
     const uint16_t* dn_w; /* packed [128/16][dim/32]                    */
     const float* dn_b;    /* [128]                                       */
+    int32_t wnt;          /* d256 8-wave 64-token kernel: expert weights
+                             read non-temporally (past the memory-side
+                             cache)                                       */
 } ExpertArgs;
 
 typedef struct ProjArgs {

@@ -148,8 +148,9 @@ struct FragSrc {
     __amdgpu_buffer_rsrc_t r;
     __device__ __forceinline__ FragSrc(const uint16_t* base, uint32_t bytes)
         : r(__builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000)) {}
+    template <int CPOL = 0>
     __device__ __forceinline__ h8 load(int frag, int lane_off) const {
-        return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, frag * 1024, 0));
+        return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, frag * 1024, CPOL));
     }
 };
 

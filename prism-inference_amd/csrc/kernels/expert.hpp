@@ -123,8 +123,9 @@ __device__ __forceinline__ void expert_stage_tile(const ExpertArgs& a, int e, in
     if (i < BM) tok[i] = t;
 }
 
-template <int DIM, int BM, int NW>
+template <int DIM, int BM, int NW, bool WNT = false>
 __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
+    constexpr int WP = WNT ? 2 : 0; /* weight loads' cache policy */
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int NT = 64 * NW;   /* threads                          */
     constexpr int KS = DIM / 32;
@@ -172,7 +173,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int r = 0; r < RT; ++r) wf[r][ks] = w1.load((wave * RT + r) * KS + ks, loff);
+            for (int r = 0; r < RT; ++r) wf[r][ks] = w1.template load<WP>((wave * RT + r) * KS + ks, loff);
         sched_fence();
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
@@ -204,7 +205,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
             for (int r = 0; r < RT; ++r) {
 #pragma unroll
                 for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
-                if (ks < KS / 2) wf[r][ks] = w2.load((wave * RT + r) * KS + ks, loff);
+                if (ks < KS / 2) wf[r][ks] = w2.template load<WP>((wave * RT + r) * KS + ks, loff);
             }
             if (ks + 1 < KS) {
 #pragma unroll
@@ -243,7 +244,7 @@ __device__ __forceinline__ void expert_body(const ExpertArgs& a) {
 #pragma unroll
                 for (int t = 0; t < TT; ++t) acc[r][t] = mfma_16x16x32(wf[r][ks], xf[t], acc[r][t]);
                 /* second half of W2, issued one half ahead of its use */
-                if (ks < KS / 2) wf[r][ks + KS / 2] = w2.load((wave * RT + r) * KS + ks + KS / 2, loff);
+                if (ks < KS / 2) wf[r][ks + KS / 2] = w2.template load<WP>((wave * RT + r) * KS + ks + KS / 2, loff);
             }
             if (ks + 1 < KS) {
 #pragma unroll
@@ -562,7 +563,10 @@ extern "C" __global__ void __launch_bounds__(256, 2) prism_expert_d128_bm64(Expe
     expert_body<128, 64, 4>(a);
 }
 extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d256_bm64_w8(ExpertArgs a) {
-    expert_body<256, 64, 8>(a);
+    if (a.wnt) /* uniform */
+        expert_body<256, 64, 8, true>(a);
+    else
+        expert_body<256, 64, 8>(a);
 }
 extern "C" __global__ void __launch_bounds__(512, 1) prism_expert_d128_bm64_w8(ExpertArgs a) {
     expert_body<128, 64, 8>(a);
