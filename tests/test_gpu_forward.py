@@ -82,6 +82,8 @@ EXTRA = {
     ("moe40", 2, 68, 120, 4),
     ("moe24d128", 3, 68, 120, 1),
     ("moe24d128", 2, 68, 120, 4),
+    ("moe64", 16, 68, 120, 1),     # the whole model (278 MB of packed weights): the leading
+                                   # blocks' expert weights stream non-temporally in the chain
     ("moe64", 2, 68, 120, 16),     # sub-chains of 8 frames: 4-wave _r4, 128-token expert tiles
                                    # (the stage calls: 96-token tiles of the same body)
     ("moe32", 2, 135, 240, 1),     # 510 windows, 8 waves, 2 router row tiles split over wave pairs
