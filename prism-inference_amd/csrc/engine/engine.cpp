@@ -111,6 +111,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_codec[4], "prism_codec_dec3"}, {&c->f_codec[5], "prism_codec_dec2"},
         {&c->f_codec[6], "prism_codec_dec1_out"}, {&c->f_codec21, "prism_codec_dec21_out"},
         {&c->f_enc01, "prism_codec_enc01"},   {&c->f_enc23, "prism_codec_enc23"},
+        {&c->f_attn_ffn[0], "prism_attn_d128_ffn"}, {&c->f_attn_ffn[1], "prism_attn_d128_w8_ffn"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);
@@ -480,10 +481,20 @@ struct RouteOut {
     int32_t* zero_next; /* counters this launch clears for a later one, or NULL */
 };
 
+/* ffn: a dense d128 block's FFN runs in the same launch (the window's rows
+ * never leave the CU between the two), and `out` receives the block's output */
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
-                 hipStream_t s, const RouteOut* route = nullptr, bool up = false) {
+                 hipStream_t s, const RouteOut* route = nullptr, bool up = false, bool ffn = false) {
     const int D = c->desc.dim;
+    if (ffn && (route || D != 128 || c->desc.n_experts != 1))
+        return fail(c, PRISM_ERR_INVALID, "the fused FFN is for dense d128 blocks");
     AttnArgs a{};
+    if (ffn) {
+        a.ffn_w1 = k.w1;
+        a.ffn_b1 = k.b1;
+        a.ffn_w2 = k.w2;
+        a.ffn_b2 = k.b2;
+    }
     if (up) { /* the adapted chain's first block: 128-channel input rows */
         a.up_w = c->up_w;
         a.up_b = c->up_b;
@@ -520,7 +531,8 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     /* fewer than two windows per CU: one 8-wave workgroup per window (a head per
      * wave) shortens each window's serial path; otherwise 4 waves x 2 per CU */
     const int w8 = grid < 512 ? 1 : 0;
-    return launch(c, c->f_attn[dim_index(D)][w8][npt], (unsigned)grid, a, s, w8 ? 512u : 256u);
+    return launch(c, ffn ? c->f_attn_ffn[w8] : c->f_attn[dim_index(D)][w8][npt], (unsigned)grid, a, s,
+                  w8 ? 512u : 256u);
 }
 
 int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {
@@ -929,6 +941,10 @@ static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int 
                 rc = enqueue_experts(c, k, attn, dst, counts, perm, n, s, CHAIN_COUNT_STRIDE, last, false,
                                      b < c->wnt_blocks);
             if (!rc) rc = timer_mark(c, tm, 1, s);
+            if (rc) return rc;
+        } else if (D == 128 && !last) { /* one launch: attention + the FFN */
+            int rc = enqueue_attn(c, k, src, dst, H, W, nf, s, nullptr, first, true);
+            if (!rc) rc = timer_mark(c, tm, 0, s);
             if (rc) return rc;
         } else {
             int rc = enqueue_attn(c, k, src, attn, H, W, nf, s, nullptr, first);

@@ -54,6 +54,11 @@ typedef struct AttnArgs {
     const uint16_t* up_w; /* packed [dim/16][128/32]                    */
     const float* up_b;    /* [dim]                                       */
     int64_t in_frame_elems; /* H*W*dim, or H*W*128 with up_w               */
+    /* fused dense FFN (prism_attn_d128[_w8]_ffn): the block's expert 0 */
+    const uint16_t* ffn_w1; /* packed [dim/16][dim/32], LN2 folded in    */
+    const float* ffn_b1;  /* [dim]                                       */
+    const uint16_t* ffn_w2; /* packed [dim/16][dim/32]                   */
+    const float* ffn_b2;  /* [dim]                                       */
 } AttnArgs;
 
 /* Router stage: at most this many 16-token tiles per wave (the LDS tables

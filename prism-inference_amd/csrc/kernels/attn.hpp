@@ -123,7 +123,7 @@ struct AttnLds {
  * O, the out-projection, LN1 (and the fused up-projection) and the routing
  * for tiles 0 and 1 only; every stored value is computed as in the full
  * body. */
-template <int DIM, int HD, int NW, int NPT, bool PAD, bool HALF = false>
+template <int DIM, int HD, int NW, int NPT, bool PAD, bool HALF = false, bool FFN = false>
 __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM, NPT>& L,
                                                  unsigned long long vmask) {
     constexpr int TQ = HALF ? 2 : 4; /* token tiles that hold tokens */
@@ -677,10 +677,122 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         }
     }
 
+    /* ---- 7. fused dense FFN (dense blocks of the d128 chain): the window's
+     * y rows are the FFN block's input h, already in os. The same
+     * arithmetic in the same order as the expert kernel's dense path
+     * (moe_expert_skip.comp.glsl:25-54 for expert 0): hn = r16(LN2(h)) (the
+     * affine folded into W1/b1), u = r16(W1 hn + b1), g = r16(GELU(u)),
+     * y2 = r16(W2 g + b2), out = y2 + h in fp16, so the output equals the
+     * attention launch followed by the expert launch bit for bit. */
+    if constexpr (FFN) {
+        static_assert(NPT == 0, "dense blocks only");
+        constexpr int RT = DIM / 16 / NW; /* hidden / output row tiles per wave */
+        static_assert(RT >= 1, "FFN shape");
+        const FragSrc w1(a.ffn_w1, DIM * DIM * 2u), w2(a.ffn_w2, DIM * DIM * 2u);
+        h8 wf[RT][KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int r = 0; r < RT; ++r) wf[r][ks] = w1.load((wave * RT + r) * KS + ks, loff);
+        /* LN2 of the window's slots into xs (dead since the out-projection),
+         * the rows each wave normalised in LN1 */
+        if (lnw) {
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int row = (wave * SPW + it * SPI + lane / LPS) * LDS;
+                const int ca = (lane % LPS) * 8;
+                const RowChunk hr{*reinterpret_cast<const h8*>(os + row + ca),
+                                  *reinterpret_cast<const h8*>(os + row + ca + DIM / 2)};
+                ln_store<DIM>(hr, valid[it], xs + row, nullptr);
+            }
+        }
+        __syncthreads();
+        f4 facc[RT][4]; /* starts at b1 */
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int ch = (wave * RT + r) * 16 + 4 * g;
+            const f4 bb = {a.ffn_b1[ch], a.ffn_b1[ch + 1], a.ffn_b1[ch + 2], a.ffn_b1[ch + 3]};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) facc[r][t] = bb;
+        }
+        h8 ff[4], fn[4];
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) ff[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t)
+                    fn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[r][ks], ff[t], facc[r][t]);
+                wf[r][ks] = w2.load((wave * RT + r) * KS + ks, loff); /* W2 in its place */
+            }
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t) ff[t] = fn[t];
+            }
+            sched_fence();
+        }
+        __syncthreads(); /* every wave is done reading the LN2 tile */
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int ch = (wave * RT + r) * 16 + 4 * g;
+            const f4 bb = {a.ffn_b2[ch], a.ffn_b2[ch + 1], a.ffn_b2[ch + 2], a.ffn_b2[ch + 3]};
+#pragma unroll
+            for (int t = 0; t < TQ; ++t) {
+                const h4 u = cvt_h4(facc[r][t]); /* r16(W1 hn + b1) */
+                f4 gl;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gl[i] = gelu_tanh_h(u[i]);
+                *reinterpret_cast<h4*>(xs + (16 * t + l16) * LDS + ch) = cvt_h4(gl);
+                facc[r][t] = bb; /* GEMM2 starts at b2 */
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) ff[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 8 * g);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t)
+                    fn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[r][ks], ff[t], facc[r][t]);
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t) ff[t] = fn[t];
+            }
+            sched_fence();
+        }
+        /* out = r16(W2 g + b2) + h in fp16, over h in os (every residual read
+           before the first add) */
+        h4 hres[4][RT];
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                hres[t][r] = *reinterpret_cast<const h4*>(os + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g);
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                *reinterpret_cast<h4*>(os + (16 * t + l16) * LDS + (wave * RT + r) * 16 + 4 * g) =
+                    add_f16x4(cvt_h4(facc[r][t]), hres[t][r]);
+        __syncthreads(); /* the block's output tile complete in os */
+    }
+
     if constexpr (NPT == 0 || NW == 8) store_rows();
 }
 
-template <int DIM, int HD, int NW, int NPT>
+template <int DIM, int HD, int NW, int NPT, bool FFN = false>
 __device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>& L) {
     const int wi = blockIdx.x % a.windows_per_frame;
     const int wy = wi / a.wx, wxx = wi - (wi / a.wx) * a.wx;
@@ -689,13 +801,13 @@ __device__ __forceinline__ void attn_window(const AttnArgs& a, AttnLds<DIM, NPT>
     const bool half = (vmask >> 32) == 0ull; /* uniform */
     if (a.bqkv_pad != nullptr && vmask != ~0ull) {
         if (half)
-            attn_window_body<DIM, HD, NW, NPT, true, true>(a, L, vmask);
+            attn_window_body<DIM, HD, NW, NPT, true, true, FFN>(a, L, vmask);
         else
-            attn_window_body<DIM, HD, NW, NPT, true>(a, L, vmask);
+            attn_window_body<DIM, HD, NW, NPT, true, false, FFN>(a, L, vmask);
     } else if (half) {
-        attn_window_body<DIM, HD, NW, NPT, false, true>(a, L, vmask);
+        attn_window_body<DIM, HD, NW, NPT, false, true, FFN>(a, L, vmask);
     } else {
-        attn_window_body<DIM, HD, NW, NPT, false>(a, L, vmask);
+        attn_window_body<DIM, HD, NW, NPT, false, false, FFN>(a, L, vmask);
     }
 }
 
@@ -721,4 +833,15 @@ PRISM_ATTN_KERNELS(128, 16, 1, _r1)
 PRISM_ATTN_KERNELS(128, 16, 2, _r2)
 PRISM_ATTN_KERNELS(128, 16, 3, _r3)
 PRISM_ATTN_KERNELS(128, 16, 4, _r4)
+
+/* d128 dense blocks in the chain: attention with the block's FFN fused
+ * (the chain's one launch per dense d128 block) */
+extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128_ffn(AttnArgs a) {
+    __shared__ AttnLds<128, 0> lds;
+    attn_window<128, 16, 4, 0, true>(a, lds);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d128_w8_ffn(AttnArgs a) {
+    __shared__ AttnLds<128, 0> lds;
+    attn_window<128, 16, 8, 0, true>(a, lds);
+}
 #undef PRISM_ATTN_KERNELS

@@ -136,6 +136,49 @@ def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, ba
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name,nb,H,W,batch,affine", [
+    ("dense128", 3, 68, 120, 1, False),   # 8-wave fused kernel; the bottom windows hold 4 rows
+    ("dense128", 2, 68, 120, 16, False),  # sub-chains of 8 frames: 4-wave fused kernel
+    ("dense128", 2, 60, 90, 4, True),     # ragged windows on both edges with LN1 beta != 0
+                                          # (the padded-slot bodies), LN2 affine folded into W1
+    ("dense128", 2, 68, 120, 1, True),
+    ("std256", 2, 68, 120, 2, False),     # d256 dense blocks keep two launches
+])
+def test_dense_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch, affine):
+    """Dense d128 blocks run attention and the FFN in one chain launch; the
+    stage calls run them as two. Same fp16 inputs and the same arithmetic in
+    the same order, so the block outputs must be identical."""
+    from test_gpu_ln_affine import with_affine
+    cfg = P.CONFIGS[name]
+    desc = cfg.desc(n_blocks=nb, H=H, W=W)
+    blob, offs = P.synth_weights(desc, seed=4, routing=cfg.routing)
+    if affine:
+        blob = with_affine(blob, offs, cfg.dim, seed=6)
+    engine.load_weights(desc, blob, offs)
+    n, d = batch * H * W, cfg.dim
+    x = P.synth_features(cfg, batch=batch, H=H, W=W, seed=5).reshape(n, d)
+    dx, dy = device_arena(n * d * 2), device_arena(n * d * 2)
+    hip.upload(dx.ptr, x)
+    print(f"[dense chain] {name} {nb} blocks {H}x{W} batch {batch} affine {affine}", flush=True)
+    engine.forward(dx.ptr, dy.ptr, batch)
+    hip.sync()
+    y_chain = hip.download(np.empty(n * d, np.uint16), dy.ptr)
+
+    feats = device_arena(3 * n * d * 2)
+    hip.upload(feats.ptr, x)
+    cur, nxt = 0, 2 * n * d
+    for b in range(nb):
+        assert engine.attn(engine.attn_push(b, cur, n * d, H, W), feats.ptr, batch) == 0, engine.error()
+        push = engine.expert_push(b, H * W, n * d, nxt)  # dense: every token, expert 0
+        assert engine.experts(push, feats.ptr, None, batch) == 0, engine.error()
+        cur, nxt = nxt, cur
+    hip.sync()
+    y_stage = hip.download(np.empty(n * d, np.uint16), feats.ptr + cur * 2)
+    assert np.isfinite(f16(y_stage)).all()
+    assert (y_stage == y_chain).all(), f"{int((y_stage != y_chain).sum())} output values differ"
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,nb,H,W,batch", [
     ("moe64", 4, 68, 120, 1),
     ("moe32", 2, 135, 240, 1),
