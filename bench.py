@@ -286,15 +286,18 @@ def config_section(hip, name, batch, steps, stream):
     tok_launch = batch * T // S
     a_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * tok_launch
     e_flops = 2 * 2 * d * d * tok_launch
-    kern = f"prism_attn_d{d}" + ("_w8" if ga < 512 else "") + (f"_r{(cfg.n_experts + 15) // 16}" if cfg.n_experts > 1 else "")
+    fused = ge == 0  # dense d128 blocks: the FFN runs inside the attention launch
+    if fused:
+        a_flops += e_flops
+    kern = f"prism_attn_d{d}" + ("_w8" if ga < 512 else "") + (f"_r{(cfg.n_experts + 15) // 16}" if cfg.n_experts > 1 else "") + ("_ffn" if fused else "")
     return {"batch": batch, "ms_per_step": round(ms_b, 5), "frames_per_s": round(batch / (ms_b * 1e-3), 2),
             "mfma_frac": round(flops_frame * batch / (ms_b * 1e-3) / MFMA_F16_PEAK, 4),
             "batch1_us_per_frame": round(ms_1 * 1e3, 2),
             "batch1_mfma_frac": round(flops_frame / (ms_1 * 1e-3) / MFMA_F16_PEAK, 4),
             "roofline": {"kernel": kern, "grid": ga, "avg_launch_ms": round(ta, 5),
                          "frac": round(a_flops / (ta * 1e-3) / MFMA_F16_PEAK, 4),
-                         "expert_grid": ge, "expert_avg_launch_ms": round(te, 5),
-                         "expert_frac": round(e_flops / (te * 1e-3) / MFMA_F16_PEAK, 4)},
+                         "expert_grid": ge, "expert_avg_launch_ms": None if fused else round(te, 5),
+                         "expert_frac": None if fused else round(e_flops / (te * 1e-3) / MFMA_F16_PEAK, 4)},
             "workload": f"d{d} x {cfg.n_blocks} blocks, {cfg.n_heads}x{cfg.head_dim} heads, "
                         + (f"{cfg.n_experts} experts top-1, " if cfg.n_experts > 1 else "dense FFN, ")
                         + f"{cfg.H}x{cfg.W} tokens"}
@@ -396,8 +399,12 @@ def main():
     tok_launch = n // S
     c_attn_flops = (attn_flops_per_token(cfg) + router_flops_per_token(cfg)) * tok_launch
     c_exp_flops = 2 * 2 * d * d * tok_launch
-    c_kname = f"prism_attn_d{d}" + ("_w8" if c_ga < 512 else "") + (f"_r{(N + 15) // 16}" if moe else "")
-    c_ename = expert_kernel(d, tok_launch, N)
+    c_fused = c_ge == 0  # dense d128 blocks: the FFN runs inside the attention launch
+    if c_fused:
+        c_attn_flops, c_exp_flops = c_attn_flops + c_exp_flops, 0
+    c_kname = (f"prism_attn_d{d}" + ("_w8" if c_ga < 512 else "") + (f"_r{(N + 15) // 16}" if moe else "")
+               + ("_ffn" if c_fused else ""))
+    c_ename = None if c_fused else expert_kernel(d, tok_launch, N)
     c_traffic, c_traffic_src = measured_traffic(c_kname, c_ga) if cfg.name == "moe64" else (None, None)
     c_etraffic, _ = measured_traffic(c_ename, c_ge) if cfg.name == "moe64" else (None, None)
 
@@ -488,7 +495,8 @@ def main():
                                        "avg_launch_ms": round(c_attn, 5),
                                        "frac": round(c_attn_flops / (c_attn * 1e-3) / MFMA_F16_PEAK, 4),
                                        "traffic": c_traffic},
-                         "experts": {"kernel": c_ename, "grid": c_ge, "flops": c_exp_flops,
+                         "experts": None if c_fused else {
+                                     "kernel": c_ename, "grid": c_ge, "flops": c_exp_flops,
                                      "avg_launch_ms": round(c_exp, 5),
                                      "frac": round(c_exp_flops / (c_exp * 1e-3) / MFMA_F16_PEAK, 4),
                                      "traffic": c_etraffic},

@@ -24,8 +24,10 @@ def test_bench_dense_config_line():
     assert out["value"] > 0 and out["ms_per_step"] > 0
     assert out["config"]["batch"] == 2 and out["config"]["experts"] == 1
     assert "dense FFN" in out["config"]["workload"]
-    assert out["roofline"]["kernel"] == "prism_attn_d128_w8"  # 270 windows: the 8-wave kernel
+    # 270 windows: the 8-wave kernel, with the block's FFN in the same launch
+    assert out["roofline"]["kernel"] == "prism_attn_d128_w8_ffn"
     assert 0 < out["roofline"]["frac"] < 1
+    assert out["roofline"]["chain_launches"]["experts"] is None
     assert out["stages_ms"]["attention_routed"] is None and out["stages_ms"]["router_stage"] is None
     assert out["stages_ms"]["experts"] > 0 and out["stages_ms"]["attention_stage"] > 0
     assert out["expert_load"] is None
