@@ -142,6 +142,8 @@ def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, ba
     ("dense128", 2, 60, 90, 4, True),     # ragged windows on both edges with LN1 beta != 0
                                           # (the padded-slot bodies), LN2 affine folded into W1
     ("dense128", 2, 68, 120, 1, True),
+    ("dense128", 2, 60, 90, 16, True),    # 4-wave fused kernel (768 windows per sub-chain) on the
+                                          # padded-slot and HALF+padded bodies
     ("std256", 2, 68, 120, 2, False),     # d256 dense blocks keep two launches
 ])
 def test_dense_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch, affine):
