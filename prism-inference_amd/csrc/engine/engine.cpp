@@ -111,7 +111,8 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_codec[4], "prism_codec_dec3"}, {&c->f_codec[5], "prism_codec_dec2"},
         {&c->f_codec[6], "prism_codec_dec1_out"}, {&c->f_codec21, "prism_codec_dec21_out"},
         {&c->f_enc01, "prism_codec_enc01"},   {&c->f_enc23, "prism_codec_enc23"},
-        {&c->f_attn_ffn[0], "prism_attn_d128_ffn"}, {&c->f_attn_ffn[1], "prism_attn_d128_w8_ffn"},
+        {&c->f_attn_ffn[0][0], "prism_attn_d128_ffn"}, {&c->f_attn_ffn[0][1], "prism_attn_d128_w8_ffn"},
+        {&c->f_attn_ffn[1][1], "prism_attn_d256_w8_ffn"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);
@@ -481,13 +482,14 @@ struct RouteOut {
     int32_t* zero_next; /* counters this launch clears for a later one, or NULL */
 };
 
-/* ffn: a dense d128 block's FFN runs in the same launch (the window's rows
- * never leave the CU between the two), and `out` receives the block's output */
+/* ffn: a dense block's FFN runs in the same launch (the window's rows never
+ * leave the CU between the two), and `out` receives the block's output; d128
+ * at every grid, d256 at the 8-wave grids (below 512 windows) */
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
                  hipStream_t s, const RouteOut* route = nullptr, bool up = false, bool ffn = false) {
     const int D = c->desc.dim;
-    if (ffn && (route || D != 128 || c->desc.n_experts != 1))
-        return fail(c, PRISM_ERR_INVALID, "the fused FFN is for dense d128 blocks");
+    if (ffn && (route || c->desc.n_experts != 1))
+        return fail(c, PRISM_ERR_INVALID, "the fused FFN is for dense blocks");
     AttnArgs a{};
     if (ffn) {
         a.ffn_w1 = k.w1;
@@ -531,8 +533,9 @@ int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* 
     /* fewer than two windows per CU: one 8-wave workgroup per window (a head per
      * wave) shortens each window's serial path; otherwise 4 waves x 2 per CU */
     const int w8 = grid < 512 ? 1 : 0;
-    return launch(c, ffn ? c->f_attn_ffn[w8] : c->f_attn[dim_index(D)][w8][npt], (unsigned)grid, a, s,
-                  w8 ? 512u : 256u);
+    const hipFunction_t f = ffn ? c->f_attn_ffn[dim_index(D)][w8] : c->f_attn[dim_index(D)][w8][npt];
+    if (!f) return fail(c, PRISM_ERR_INVALID, "no fused FFN kernel for d%d at %lld windows", D, (long long)grid);
+    return launch(c, f, (unsigned)grid, a, s, w8 ? 512u : 256u);
 }
 
 int enqueue_zero(prism_ctx* c, int32_t* p, int32_t n, hipStream_t s) {
@@ -942,7 +945,10 @@ static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int 
                                      b < c->wnt_blocks);
             if (!rc) rc = timer_mark(c, tm, 1, s);
             if (rc) return rc;
-        } else if (D == 128 && !last) { /* one launch: attention + the FFN */
+        } else if (!last && (D == 128 || (int64_t)((W + 7) / 8) * ((H + 7) / 8) * nf < 512)) {
+            /* one launch: attention + the FFN (d256: 8-wave grids only, where a
+               64-token window's share of the FFN weights matches the 64-token
+               expert tiles those grids use) */
             int rc = enqueue_attn(c, k, src, dst, H, W, nf, s, nullptr, first, true);
             if (!rc) rc = timer_mark(c, tm, 0, s);
             if (rc) return rc;

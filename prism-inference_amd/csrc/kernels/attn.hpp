@@ -834,8 +834,8 @@ PRISM_ATTN_KERNELS(128, 16, 2, _r2)
 PRISM_ATTN_KERNELS(128, 16, 3, _r3)
 PRISM_ATTN_KERNELS(128, 16, 4, _r4)
 
-/* d128 dense blocks in the chain: attention with the block's FFN fused
- * (the chain's one launch per dense d128 block) */
+/* dense blocks in the chain: attention with the block's FFN fused (the
+ * chain's one launch per dense block; d256 only at the 8-wave grids) */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128_ffn(AttnArgs a) {
     __shared__ AttnLds<128, 0> lds;
     attn_window<128, 16, 4, 0, true>(a, lds);
@@ -843,5 +843,9 @@ extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128_ffn(AttnArg
 extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d128_w8_ffn(AttnArgs a) {
     __shared__ AttnLds<128, 0> lds;
     attn_window<128, 16, 8, 0, true>(a, lds);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d256_w8_ffn(AttnArgs a) {
+    __shared__ AttnLds<256, 0> lds;
+    attn_window<256, 32, 8, 0, true>(a, lds);
 }
 #undef PRISM_ATTN_KERNELS

@@ -3,7 +3,8 @@ runs exactly the chain's launches: its output equals prism_forward's bit for
 bit, and it reports the grids the chain launches (attention: one workgroup
 per 8x8 window of a sub-chain's frames; experts: the 128-token tiles of a
 d256 sub-chain of 8 frames, 64-token 8-wave tiles at batch 1; dense d128
-blocks run their FFN inside the attention launch, so no expert launch)."""
+blocks, and dense d256 blocks below 512 windows, run their FFN inside the
+attention launch, so no expert launch)."""
 import numpy as np
 import pytest
 
@@ -15,7 +16,8 @@ import prism_amd as P
     ("moe64", 2, 16, 1080, 576),   # two sub-chains of 8 frames: 8 x 135 windows; 510 + 64 tiles -> 576
     ("moe64", 2, 1, 135, 192),     # one frame: 8-wave kernels, 128 + 64 tiles -> 192
     ("dense128", 2, 4, 270, 0),    # two sub-chains of 2 frames; attention + FFN in one launch
-    ("std256", 2, 2, 270, 256),    # one sub-chain of 2 frames; d256 dense: 255 tiles -> 256
+    ("std256", 2, 2, 270, 0),      # one sub-chain of 2 frames: 8-wave d256 attention + FFN in one launch
+    ("std256", 2, 16, 1080, 512),  # two sub-chains of 8 frames: d256 dense FFN in 128-token tiles
 ])
 def test_chain_launch_times_run_the_chain(hip, engine, device_arena, name, nb, batch, attn_grid, expert_grid):
     cfg = P.CONFIGS[name]
