@@ -91,7 +91,7 @@ struct prism_ctx {
     int device = 0;
     hipModule_t module = nullptr;
     hipFunction_t f_attn[2][2][5] = {}; /* [d128, d256][4 waves, 8 waves][routed: padded experts / 16] */
-    hipFunction_t f_attn_ffn[2][2] = {}; /* dense blocks, FFN fused: [d128, d256][4 waves, 8 waves]; no d256 4-wave */
+    hipFunction_t f_attn_ffn[2][2] = {}; /* dense blocks, FFN fused: [d128, d256][4 waves, 8 waves] */
     hipFunction_t f_router[2][4] = {};  /* [dim][padded experts / 16 - 1] */
     hipFunction_t f_expert[2][2] = {};  /* [dim][4 waves, 8 waves], 64-token tiles */
     hipFunction_t f_expert_wide = nullptr; /* d256, 128-token tiles */

@@ -112,7 +112,7 @@ extern "C" int prism_create(prism_ctx** out, int32_t device, const char* code_ob
         {&c->f_codec[6], "prism_codec_dec1_out"}, {&c->f_codec21, "prism_codec_dec21_out"},
         {&c->f_enc01, "prism_codec_enc01"},   {&c->f_enc23, "prism_codec_enc23"},
         {&c->f_attn_ffn[0][0], "prism_attn_d128_ffn"}, {&c->f_attn_ffn[0][1], "prism_attn_d128_w8_ffn"},
-        {&c->f_attn_ffn[1][1], "prism_attn_d256_w8_ffn"},
+        {&c->f_attn_ffn[1][0], "prism_attn_d256_ffn"}, {&c->f_attn_ffn[1][1], "prism_attn_d256_w8_ffn"},
     };
     std::vector<std::pair<hipFunction_t*, std::string>> all;
     for (auto& f : fns) all.emplace_back(f.f, f.name);
@@ -483,8 +483,7 @@ struct RouteOut {
 };
 
 /* ffn: a dense block's FFN runs in the same launch (the window's rows never
- * leave the CU between the two), and `out` receives the block's output; d128
- * at every grid, d256 at the 8-wave grids (below 512 windows) */
+ * leave the CU between the two), and `out` receives the block's output */
 int enqueue_attn(prism_ctx* c, const DevBlock& k, const uint16_t* in, uint16_t* out, int H, int W, int batch,
                  hipStream_t s, const RouteOut* route = nullptr, bool up = false, bool ffn = false) {
     const int D = c->desc.dim;
@@ -945,10 +944,7 @@ static int enqueue_subchain(prism_ctx* c, const ChainWs& ws, int j, int f0, int 
                                      b < c->wnt_blocks);
             if (!rc) rc = timer_mark(c, tm, 1, s);
             if (rc) return rc;
-        } else if (!last && (D == 128 || (int64_t)((W + 7) / 8) * ((H + 7) / 8) * nf < 512)) {
-            /* one launch: attention + the FFN (d256: 8-wave grids only, where a
-               64-token window's share of the FFN weights matches the 64-token
-               expert tiles those grids use) */
+        } else if (!last) { /* one launch: attention + the FFN */
             int rc = enqueue_attn(c, k, src, dst, H, W, nf, s, nullptr, first, true);
             if (!rc) rc = timer_mark(c, tm, 0, s);
             if (rc) return rc;

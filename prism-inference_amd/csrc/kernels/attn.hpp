@@ -689,11 +689,19 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
         constexpr int RT = DIM / 16 / NW; /* hidden / output row tiles per wave */
         static_assert(RT >= 1, "FFN shape");
         const FragSrc w1(a.ffn_w1, DIM * DIM * 2u), w2(a.ffn_w2, DIM * DIM * 2u);
-        h8 wf[RT][KS];
+        /* the wave's weight stream: W1 then W2, k-step-major over its RT row
+         * tiles, through a ring of FR fragments (all of W1 when that is at
+         * most 16 fragments, W2 then refilling the slots GEMM1 frees; else
+         * 3 k-steps ahead) */
+        constexpr int NFF = 2 * RT * KS;
+        constexpr int FR = RT * KS <= 16 ? RT * KS : 3 * RT;
+        auto ffrag = [&](int p) -> h8 {
+            const int q = p % (RT * KS), ks = q / RT, r = q % RT;
+            return (p < RT * KS ? w1 : w2).load((wave * RT + r) * KS + ks, loff);
+        };
+        h8 wf[FR];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int r = 0; r < RT; ++r) wf[r][ks] = w1.load((wave * RT + r) * KS + ks, loff);
+        for (int p = 0; p < FR; ++p) wf[p] = ffrag(p);
         /* LN2 of the window's slots into xs (dead since the out-projection),
          * the rows each wave normalised in LN1 */
         if (lnw) {
@@ -727,9 +735,10 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
             }
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
+                const int p = ks * RT + r;
 #pragma unroll
-                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[r][ks], ff[t], facc[r][t]);
-                wf[r][ks] = w2.load((wave * RT + r) * KS + ks, loff); /* W2 in its place */
+                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[p % FR], ff[t], facc[r][t]);
+                if (p + FR < NFF) wf[p % FR] = ffrag(p + FR);
             }
             if (ks + 1 < KS) {
 #pragma unroll
@@ -763,9 +772,12 @@ __device__ __forceinline__ void attn_window_body(const AttnArgs& a, AttnLds<DIM,
                     fn[t] = *reinterpret_cast<const h8*>(xs + (16 * t + l16) * LDS + 32 * (ks + 1) + 8 * g);
             }
 #pragma unroll
-            for (int r = 0; r < RT; ++r)
+            for (int r = 0; r < RT; ++r) {
+                const int p = RT * KS + ks * RT + r;
 #pragma unroll
-                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[r][ks], ff[t], facc[r][t]);
+                for (int t = 0; t < TQ; ++t) facc[r][t] = mfma_16x16x32(wf[p % FR], ff[t], facc[r][t]);
+                if (p + FR < NFF) wf[p % FR] = ffrag(p + FR);
+            }
             if (ks + 1 < KS) {
 #pragma unroll
                 for (int t = 0; t < TQ; ++t) ff[t] = fn[t];
@@ -835,7 +847,7 @@ PRISM_ATTN_KERNELS(128, 16, 3, _r3)
 PRISM_ATTN_KERNELS(128, 16, 4, _r4)
 
 /* dense blocks in the chain: attention with the block's FFN fused (the
- * chain's one launch per dense block; d256 only at the 8-wave grids) */
+ * chain's one launch per dense block) */
 extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128_ffn(AttnArgs a) {
     __shared__ AttnLds<128, 0> lds;
     attn_window<128, 16, 4, 0, true>(a, lds);
@@ -843,6 +855,10 @@ extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d128_ffn(AttnArg
 extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d128_w8_ffn(AttnArgs a) {
     __shared__ AttnLds<128, 0> lds;
     attn_window<128, 16, 8, 0, true>(a, lds);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) prism_attn_d256_ffn(AttnArgs a) {
+    __shared__ AttnLds<256, 0> lds;
+    attn_window<256, 32, 4, 0, true>(a, lds);
 }
 extern "C" __global__ void __launch_bounds__(512, 1) prism_attn_d256_w8_ffn(AttnArgs a) {
     __shared__ AttnLds<256, 0> lds;

@@ -2,9 +2,8 @@
 runs exactly the chain's launches: its output equals prism_forward's bit for
 bit, and it reports the grids the chain launches (attention: one workgroup
 per 8x8 window of a sub-chain's frames; experts: the 128-token tiles of a
-d256 sub-chain of 8 frames, 64-token 8-wave tiles at batch 1; dense d128
-blocks, and dense d256 blocks below 512 windows, run their FFN inside the
-attention launch, so no expert launch)."""
+d256 sub-chain of 8 frames, 64-token 8-wave tiles at batch 1; dense blocks
+run their FFN inside the attention launch, so no expert launch)."""
 import numpy as np
 import pytest
 
@@ -17,7 +16,7 @@ import prism_amd as P
     ("moe64", 2, 1, 135, 192),     # one frame: 8-wave kernels, 128 + 64 tiles -> 192
     ("dense128", 2, 4, 270, 0),    # two sub-chains of 2 frames; attention + FFN in one launch
     ("std256", 2, 2, 270, 0),      # one sub-chain of 2 frames: 8-wave d256 attention + FFN in one launch
-    ("std256", 2, 16, 1080, 512),  # two sub-chains of 8 frames: d256 dense FFN in 128-token tiles
+    ("std256", 2, 16, 1080, 0),    # two sub-chains of 8 frames: 4-wave attention + FFN in one launch
 ])
 def test_chain_launch_times_run_the_chain(hip, engine, device_arena, name, nb, batch, attn_grid, expert_grid):
     cfg = P.CONFIGS[name]

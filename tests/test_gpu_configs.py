@@ -44,12 +44,14 @@ def subchain_batches(batch):
     return [batch // 2, batch - batch // 2]
 
 
-def attn_kernel(dim, n_experts, windows):
+def attn_kernel(dim, n_experts, windows, chain=False):
     """The attention kernel the engine launches for a grid of `windows`
     workgroups: 8 waves below 512 windows, 4 waves from 512 on; _r<k> routes
-    over 16k padded experts."""
+    over 16k padded experts; _ffn: a dense block of the chain, its FFN in the
+    same launch."""
     npt = (n_experts + 15) // 16 if n_experts > 1 else 0
-    return f"prism_attn_d{dim}{'_w8' if windows < 512 else ''}{f'_r{npt}' if npt else ''}"
+    return (f"prism_attn_d{dim}{'_w8' if windows < 512 else ''}{f'_r{npt}' if npt else ''}"
+            + ("_ffn" if chain and not npt else ""))
 
 
 @pytest.mark.gpu
@@ -57,14 +59,14 @@ def attn_kernel(dim, n_experts, windows):
     ("moe32", 4, "prism_attn_d256_r2"),   # 2 x 2 frames of 510 windows: the 4-wave N=32 kernel
     ("moe16", 1, "prism_attn_d256_w8_r1"),
     ("moe64", 16, "prism_attn_d256_r4"),  # the headline step: 2 x 8 frames, 1080 windows each
-    ("dense128", 16, "prism_attn_d128"),  # 2 x 8 frames of 1080 windows, dense FFN
-    ("std256", 16, "prism_attn_d256"),    # 2 x 8 frames: the dense FFN in 128-token tiles
+    ("dense128", 16, "prism_attn_d128_ffn"),  # 2 x 8 frames of 1080 windows, FFN in the launch
+    ("std256", 16, "prism_attn_d256_ffn"),    # 2 x 8 frames, FFN in the launch
 ])
 def test_config_chain_against_oracle(hip, engine, device_arena, name, batch, kernel):
     cfg = P.CONFIGS[name]
     H, W, nb = cfg.H, cfg.W, cfg.n_blocks
     windows = ((H + 7) // 8) * ((W + 7) // 8)
-    assert attn_kernel(cfg.dim, cfg.n_experts, windows * subchain_batches(batch)[0]) == kernel
+    assert attn_kernel(cfg.dim, cfg.n_experts, windows * subchain_batches(batch)[0], chain=True) == kernel
     desc = cfg.desc()
     blob, offs = P.synth_weights(desc, seed=0, routing=cfg.routing)
     engine.load_weights(desc, blob, offs)

@@ -144,13 +144,14 @@ def test_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, ba
     ("dense128", 2, 68, 120, 1, True),
     ("dense128", 2, 60, 90, 16, True),    # 4-wave fused kernel (768 windows per sub-chain) on the
                                           # padded-slot and HALF+padded bodies
-    ("std256", 2, 68, 120, 2, False),     # d256: fused at the 8-wave grids (270 windows)
+    ("std256", 2, 68, 120, 2, False),     # d256, 8-wave fused kernel (270 windows)
     ("std256", 2, 68, 120, 1, True),
-    ("std256", 2, 68, 120, 16, False),    # 1080 windows per sub-chain: two launches
+    ("std256", 2, 68, 120, 16, False),    # 1080 windows per sub-chain: 4-wave fused kernel
+    ("std256", 2, 60, 90, 16, True),      # 4-wave, padded-slot and HALF+padded bodies
 ])
 def test_dense_chain_matches_stage_calls(hip, engine, device_arena, name, nb, H, W, batch, affine):
-    """Dense blocks run attention and the FFN in one chain launch (d128 at
-    every grid, d256 below 512 windows); the stage calls run them as two. Same fp16 inputs and the same arithmetic in
+    """Dense blocks run attention and the FFN in one chain launch; the stage
+    calls run them as two. Same fp16 inputs and the same arithmetic in
     the same order, so the block outputs must be identical."""
     from test_gpu_ln_affine import with_affine
     cfg = P.CONFIGS[name]
