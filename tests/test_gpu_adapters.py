@@ -162,6 +162,8 @@ def test_adapted_chain(hip, engine, device_arena, name, nb, H, W, batch, affine)
     ("moe64", 2, 68, 120, 4, True),    # 4 waves
     ("moe16", 1, 20, 28, 4, True),     # ragged right and bottom windows, one block
     ("dense128", 2, 68, 120, 2, True),
+    ("std256", 2, 68, 120, 16, True),  # 4-wave d256 attention with the up-projection and the FFN
+    ("std256", 2, 68, 120, 1, True),   # the same in 8 waves
 ])
 def test_fused_adapters_equal_the_separate_calls(hip, engine, device_arena, name, nb, H, W, batch, affine):
     """The adapted chain fuses the up-projection into the first block's
