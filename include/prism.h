@@ -251,7 +251,9 @@ int prism_forward_noalloc(prism_ctx* ctx, const void* in, void* out, int32_t bat
  * launches, waits for them, and returns the mean duration in ms of the
  * chain's attention launches (attn_ms) and of its expert launches
  * (expert_ms), and the workgroup count of each (the first launch of each
- * kind). `out` receives the chain's output, as from prism_forward. */
+ * kind). A dense block runs its FFN inside its attention launch, so a dense
+ * model reports expert_ms = 0 and expert_grid = 0. `out` receives the
+ * chain's output, as from prism_forward. */
 int prism_chain_launch_times(prism_ctx* ctx, const void* in, void* out, int32_t batch, void* stream,
                              float* attn_ms, float* expert_ms, int32_t* attn_grid, int32_t* expert_grid);
 
