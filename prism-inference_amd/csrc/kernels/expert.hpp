@@ -9,12 +9,15 @@
  * router's buckets, so every lane computes.
  *
  * Tile scheduler: the grid is sized for the worst case (ceil(T/BM) + N tiles,
- * rounded up to a multiple of 8). Workgroup i maps to logical tile
- * (i % 8) * (grid / 8) + i / 8 so that consecutive tiles of one expert land on
- * the same XCD (hardware dispatches workgroups round-robin over the 8 XCDs)
- * and share that XCD's L2 copy of the expert's weights. Every wave turns the
- * per-expert counts into a tile prefix sum (a DPP scan) and finds its
- * (expert, row block) itself; tiles past the end do nothing.
+ * rounded up to a multiple of 8). Every wave turns the per-expert counts into
+ * a tile prefix sum (a DPP scan), whose total is the number of tiles that
+ * exist; workgroup i maps to logical tile (i % 8) * chunk + i / 8, chunk =
+ * ceil(total / 8), so that consecutive tiles of one expert land on the same
+ * XCD (hardware dispatches workgroups round-robin over the 8 XCDs) and share
+ * that XCD's L2 copy of the expert's weights, and every XCD gets an equal
+ * share of the tiles; each wave finds its (expert, row block) itself, and
+ * workgroups past the tiles do nothing. (The dense FFN stage, no counts:
+ * chunk = grid / 8.)
  *
  * Weight streaming: as soon as the tokens are gathered, each wave issues
  * every W1 fragment of its 16*RT output rows (RT*KS 1 KiB fragments, held in
@@ -75,13 +78,19 @@ __device__ __forceinline__ void expert_store_rows(uint16_t* out, const f16* tile
  * are wave-uniform. */
 template <int BM>
 __device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int lane, int& e, int& row0, int& rows) {
-    const int per_xcd = gridDim.x / 8;
-    const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (a.counts) {
         const int c = lane < a.n_experts ? min(a.counts[lane * a.count_stride], a.cap) : 0;
         const int nt = (c + BM - 1) / BM;
         const int incl = wave_incl_scan(nt);
         const int excl = incl - nt;
+        /* the tiles that exist (the grid holds the worst case), dealt to the
+         * 8 XCDs in equal contiguous chunks: workgroup i runs tile
+         * (i % 8) * chunk + i / 8, so no XCD is left with the empty end of
+         * the tile range while the others queue a second round */
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        const int per_xcd = (total + 7) / 8;
+        const int k = blockIdx.x / 8;
+        const int L = k < per_xcd ? (blockIdx.x % 8) * per_xcd + k : 0x7fffffff;
         const bool mine = lane < a.n_experts && L >= excl && L < incl;
         const unsigned long long bal = __ballot(mine); /* one lane at most */
         if (bal == 0ull) {
@@ -95,6 +104,8 @@ __device__ __forceinline__ void expert_schedule(const ExpertArgs& a, int lane, i
         row0 = (L - ex) * BM;
         rows = min(BM, co - row0);
     } else {
+        const int per_xcd = gridDim.x / 8;
+        const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
         row0 = L * BM;
         e = row0 < a.n_tokens ? 0 : -1;
         rows = min(BM, a.n_tokens - row0);
